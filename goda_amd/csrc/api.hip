@@ -1,0 +1,234 @@
+// C-ABI entry points of libgoda_attn.so: argument validation on the host,
+// then dispatch to the kernels. Nothing here allocates or synchronises.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "goda_attn.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int32_t ok() {
+  g_last_error.clear();
+  return GODA_OK;
+}
+
+int32_t hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  if (e == hipErrorNotSupported) return fail(GODA_ERR_UNSUPPORTED, "%s: no kernel instance for these arguments", what);
+  return fail(GODA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool dtype_ok(int32_t d) { return d == GODA_DTYPE_F32 || d == GODA_DTYPE_F16 || d == GODA_DTYPE_BF16; }
+
+bool head_dim_ok(int32_t d) { return d == 64 || d == 128 || d == 256; }
+
+// Checks shared by prefill; returns GODA_OK or a failure status.
+int32_t check_prefill(const goda_prefill_args* a) {
+  if (!a) return fail(GODA_ERR_INVALID_ARG, "prefill: args is NULL");
+  if (!dtype_ok(a->dtype)) return fail(GODA_ERR_INVALID_ARG, "prefill: unknown dtype %d", a->dtype);
+  if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_k < 0)
+    return fail(GODA_ERR_INVALID_ARG, "prefill: negative size (batch %d, seqlen_q %d, seqlen_k %d)",
+                a->batch, a->seqlen_q, a->seqlen_k);
+  if (a->heads_q <= 0 || a->heads_kv <= 0)
+    return fail(GODA_ERR_INVALID_ARG, "prefill: heads_q %d / heads_kv %d must be positive", a->heads_q,
+                a->heads_kv);
+  if (a->heads_q % a->heads_kv != 0)
+    return fail(GODA_ERR_INVALID_ARG, "prefill: heads_q %d is not a multiple of heads_kv %d", a->heads_q,
+                a->heads_kv);
+  if (!head_dim_ok(a->head_dim))
+    return fail(GODA_ERR_UNSUPPORTED, "prefill: head_dim %d not in {64, 128, 256}", a->head_dim);
+  if ((a->cu_seqlens_q == nullptr) != (a->cu_seqlens_k == nullptr))
+    return fail(GODA_ERR_INVALID_ARG, "prefill: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
+  if (a->batch == 0 || a->seqlen_q == 0) return GODA_OK;
+  if (!a->q || !a->k || !a->v || !a->o) return fail(GODA_ERR_INVALID_ARG, "prefill: NULL tensor pointer");
+  if (a->rope_q || a->rope_k) {
+    if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
+      return fail(GODA_ERR_INVALID_ARG, "prefill: RoPE requested without cos/sin tables");
+    // Highest position touched: q rows sit at rope_q_offset + (Lk - Lq) + i <=
+    // rope_q_offset + seqlen_k - 1 when Lq >= 1; k rows at rope_k_offset + j.
+    const int64_t qmax = (int64_t)a->rope_q_offset + a->seqlen_k - 1;
+    const int64_t kmax = (int64_t)a->rope_k_offset + a->seqlen_k - 1;
+    if (a->rope_q && (a->rope_q_offset < 0 || qmax >= a->rope_len))
+      return fail(GODA_ERR_INVALID_ARG, "prefill: q positions up to %lld exceed rope_len %d",
+                  (long long)qmax, a->rope_len);
+    if (a->rope_k && (a->rope_k_offset < 0 || kmax >= a->rope_len))
+      return fail(GODA_ERR_INVALID_ARG, "prefill: k positions up to %lld exceed rope_len %d",
+                  (long long)kmax, a->rope_len);
+    if (a->rope_q && !a->cu_seqlens_q && a->seqlen_q > a->seqlen_k && !a->seqused_k)
+      return fail(GODA_ERR_INVALID_ARG, "prefill: RoPE on q needs seqlen_q <= seqlen_k");
+  }
+  return GODA_OK;
+}
+
+goda::PrefillParams make_prefill_params(const goda_prefill_args* a) {
+  goda::PrefillParams p;
+  memset(&p, 0, sizeof(p));
+  p.a = *a;
+  p.group = a->heads_q / a->heads_kv;
+  p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t goda_attn_abi_version(void) { return GODA_ATTN_ABI_VERSION; }
+int64_t goda_attn_sizeof_prefill_args(void) { return sizeof(goda_prefill_args); }
+int64_t goda_attn_sizeof_decode_args(void) { return sizeof(goda_decode_args); }
+int64_t goda_attn_sizeof_kv_append_args(void) { return sizeof(goda_kv_append_args); }
+
+const char* goda_attn_last_error(void) { return g_last_error.c_str(); }
+
+int64_t goda_attn_prefill_workspace_size(const goda_prefill_args* a) {
+  const int32_t st = check_prefill(a);
+  if (st != GODA_OK) return st;
+  if (goda::prefill_mfma_supported(*a)) return goda::prefill_mfma_workspace_bytes(*a);
+  return 0;
+}
+
+int32_t goda_attn_prefill_fwd(const goda_prefill_args* a, void* stream) {
+  const int32_t st = check_prefill(a);
+  if (st != GODA_OK) return st;
+  if (a->batch == 0 || a->seqlen_q == 0) return ok();
+  goda::PrefillParams p = make_prefill_params(a);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (goda::prefill_mfma_supported(*a)) {
+    const int64_t need = goda::prefill_mfma_workspace_bytes(*a);
+    if (need > 0 && (!a->workspace || a->workspace_bytes < need))
+      return fail(GODA_ERR_WORKSPACE, "prefill: workspace of %lld bytes needed, %lld given",
+                  (long long)need, (long long)a->workspace_bytes);
+    return hip_status(goda::launch_prefill_mfma(p, s), "prefill_fwd");
+  }
+  return hip_status(goda::launch_prefill_generic(p, s), "prefill_fwd");
+}
+
+int64_t goda_attn_decode_workspace_size(const goda_decode_args* a) {
+  if (!a) return fail(GODA_ERR_INVALID_ARG, "decode: args is NULL");
+  if (!goda::decode_mfma_supported(*a)) return 0;
+  const int split = a->split_size > 0 ? a->split_size : goda::decode_default_split(*a);
+  return goda::decode_workspace_bytes(*a, split);
+}
+
+int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
+  if (!a) return fail(GODA_ERR_INVALID_ARG, "decode: args is NULL");
+  if (!dtype_ok(a->dtype)) return fail(GODA_ERR_INVALID_ARG, "decode: unknown dtype %d", a->dtype);
+  if (a->batch < 0 || a->max_seqlen < 0)
+    return fail(GODA_ERR_INVALID_ARG, "decode: negative size (batch %d, max_seqlen %d)", a->batch,
+                a->max_seqlen);
+  if (a->heads_q <= 0 || a->heads_kv <= 0 || a->heads_q % a->heads_kv != 0)
+    return fail(GODA_ERR_INVALID_ARG, "decode: heads_q %d must be a positive multiple of heads_kv %d",
+                a->heads_q, a->heads_kv);
+  if (!head_dim_ok(a->head_dim))
+    return fail(GODA_ERR_UNSUPPORTED, "decode: head_dim %d not in {64, 128, 256}", a->head_dim);
+  if (a->split_size < 0 || (a->split_size > 0 && a->split_size % 64 != 0))
+    return fail(GODA_ERR_INVALID_ARG, "decode: split_size %d must be 0 or a positive multiple of 64",
+                a->split_size);
+  if (a->batch == 0) return ok();
+  if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->cache_seqlens)
+    return fail(GODA_ERR_INVALID_ARG, "decode: NULL tensor pointer");
+  if (a->rope_q) {
+    if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
+      return fail(GODA_ERR_INVALID_ARG, "decode: RoPE requested without cos/sin tables");
+    if (a->rope_q_offset < 0 || (int64_t)a->rope_q_offset + a->max_seqlen - 1 >= a->rope_len)
+      return fail(GODA_ERR_INVALID_ARG, "decode: q positions up to %lld exceed rope_len %d",
+                  (long long)a->rope_q_offset + a->max_seqlen - 1, a->rope_len);
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (goda::decode_mfma_supported(*a)) {
+    goda::DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    p.a = *a;
+    p.group = a->heads_q / a->heads_kv;
+    p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+    p.split = a->split_size > 0 ? a->split_size : goda::decode_default_split(*a);
+    p.nsplit_max = a->max_seqlen > 0 ? (a->max_seqlen + p.split - 1) / p.split : 1;
+    const int64_t need = goda::decode_workspace_bytes(*a, p.split);
+    if (need > 0 && (!a->workspace || a->workspace_bytes < need))
+      return fail(GODA_ERR_WORKSPACE, "decode: workspace of %lld bytes needed, %lld given",
+                  (long long)need, (long long)a->workspace_bytes);
+    return hip_status(goda::launch_decode(p, s), "decode");
+  }
+  // Other dtypes / head dims: the generic prefill kernel with one query row
+  // per sequence and seqused_k = cache_seqlens (bottom-right alignment puts
+  // the query at position cache_seqlens[b] - 1).
+  goda_prefill_args pa;
+  memset(&pa, 0, sizeof(pa));
+  pa.dtype = a->dtype;
+  pa.batch = a->batch;
+  pa.heads_q = a->heads_q;
+  pa.heads_kv = a->heads_kv;
+  pa.head_dim = a->head_dim;
+  pa.seqlen_q = 1;
+  pa.seqlen_k = a->max_seqlen;
+  pa.causal = 1;
+  pa.window_left = a->window_left;
+  pa.softmax_scale = a->softmax_scale;
+  pa.q = a->q;
+  pa.q_stride_b = a->q_stride_b;
+  pa.q_stride_t = 0;
+  pa.q_stride_h = a->q_stride_h;
+  pa.k = a->k_cache;
+  pa.k_stride_b = a->k_stride_b;
+  pa.k_stride_t = a->k_stride_t;
+  pa.k_stride_h = a->k_stride_h;
+  pa.v = a->v_cache;
+  pa.v_stride_b = a->v_stride_b;
+  pa.v_stride_t = a->v_stride_t;
+  pa.v_stride_h = a->v_stride_h;
+  pa.o = a->o;
+  pa.o_stride_b = a->o_stride_b;
+  pa.o_stride_t = 0;
+  pa.o_stride_h = a->o_stride_h;
+  pa.lse = a->lse;
+  pa.lse_stride_b = a->lse_stride_b;
+  pa.lse_stride_h = 1;
+  pa.seqused_k = a->cache_seqlens;
+  pa.alibi_slopes = a->alibi_slopes;
+  pa.rope_cos = a->rope_cos;
+  pa.rope_sin = a->rope_sin;
+  pa.rope_len = a->rope_len;
+  pa.rope_q = a->rope_q;
+  pa.rope_q_offset = a->rope_q_offset;
+  goda::PrefillParams p = make_prefill_params(&pa);
+  return hip_status(goda::launch_prefill_generic(p, s), "decode");
+}
+
+int32_t goda_attn_kv_append(const goda_kv_append_args* a, void* stream) {
+  if (!a) return fail(GODA_ERR_INVALID_ARG, "kv_append: args is NULL");
+  if (!dtype_ok(a->dtype)) return fail(GODA_ERR_INVALID_ARG, "kv_append: unknown dtype %d", a->dtype);
+  if (a->batch < 0 || a->seqlen_new < 0 || a->heads_kv <= 0 || a->head_dim <= 0 || a->head_dim % 2 != 0)
+    return fail(GODA_ERR_INVALID_ARG, "kv_append: bad sizes (batch %d, seqlen_new %d, heads_kv %d, head_dim %d)",
+                a->batch, a->seqlen_new, a->heads_kv, a->head_dim);
+  if (a->batch == 0) return ok();
+  if (!a->k_new || !a->v_new || !a->k_cache || !a->v_cache || !a->cache_seqlens)
+    return fail(GODA_ERR_INVALID_ARG, "kv_append: NULL tensor pointer");
+  if (a->rope_k) {
+    if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
+      return fail(GODA_ERR_INVALID_ARG, "kv_append: RoPE requested without cos/sin tables");
+    if (a->rope_k_offset < 0 || (int64_t)a->rope_k_offset + a->max_seqlen - 1 >= a->rope_len)
+      return fail(GODA_ERR_INVALID_ARG, "kv_append: positions up to %lld exceed rope_len %d",
+                  (long long)a->rope_k_offset + a->max_seqlen - 1, a->rope_len);
+  }
+  return hip_status(goda::launch_kv_append(*a, reinterpret_cast<hipStream_t>(stream)), "kv_append");
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// Device-side helpers shared by the attention kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "goda_attn.h"
+
+namespace goda {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// ---- element type traits -------------------------------------------------
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float to_f32(float x) { return x; }
+  static __device__ __forceinline__ float from_f32(float x) { return x; }
+};
+
+template <>
+struct Elem<bf16> {
+  static __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+  static __device__ __forceinline__ bf16 from_f32(float x) { return (bf16)x; }
+  typedef bf16x8 vec8;
+  typedef bf16x4 vec4;
+};
+
+template <>
+struct Elem<f16> {
+  static __device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+  static __device__ __forceinline__ f16 from_f32(float x) { return (f16)x; }
+  typedef f16x8 vec8;
+  typedef f16x4 vec4;
+};
+
+// 32x32x16 MFMA with fp32 accumulation on 8-element operands.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// 16x16x32 MFMA with fp32 accumulation on 8-element operands.
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+// 16-byte and 8-byte vector memory helpers on raw element pointers.
+template <typename V, typename T>
+__device__ __forceinline__ V ld_vec(const T* p) {
+  return *reinterpret_cast<const V*>(p);
+}
+template <typename V, typename T>
+__device__ __forceinline__ void st_vec(T* p, V v) {
+  *reinterpret_cast<V*>(p) = v;
+}
+
+// Per-sequence geometry shared by every kernel: row offsets of sequence b in
+// q/k storage and its query / key counts.
+struct SeqGeom {
+  int64_t q_row0;  // first query row (varlen) or 0
+  int64_t k_row0;
+  int lq, lk;
+};
+
+__device__ __forceinline__ SeqGeom seq_geom(int b, int seqlen_q, int seqlen_k,
+                                            const int32_t* cu_q, const int32_t* cu_k,
+                                            const int32_t* seqused_k) {
+  SeqGeom g;
+  if (cu_q) {
+    g.q_row0 = cu_q[b];
+    g.lq = cu_q[b + 1] - cu_q[b];
+  } else {
+    g.q_row0 = 0;
+    g.lq = seqlen_q;
+  }
+  if (cu_k) {
+    g.k_row0 = cu_k[b];
+    g.lk = cu_k[b + 1] - cu_k[b];
+  } else {
+    g.k_row0 = 0;
+    g.lk = seqlen_k;
+  }
+  // Device-side lengths are clamped to the rows the tensors hold, so a bad
+  // value can shrink the work but never move a read out of bounds.
+  if (seqused_k) g.lk = max(0, min(seqused_k[b], g.lk));
+  return g;
+}
+
+}  // namespace goda

@@ -1,0 +1,69 @@
+"""Drop-in for goda's `kernels_` package (kernels_/__init__.py:15).
+
+`FlashAttentionGQAKernel` and `FlashAttentionMQAKernel` keep the reference's
+autograd signature `apply(Q, K, V, causal, tau) -> O` on [B, H, T, D] tensors
+(kernels_/flash_attn_gqa/cuda.py:515-575, kernels_/flash_attn_mqa/cuda.py:470-527),
+and extend it compatibly:
+  - K and V may carry Hkv heads with Hkv | Hq (query head h reads KV head
+    h // (Hq/Hkv)); the reference indexes K/V with Q's head and so only
+    handles Hq == Hkv (kernels_/flash_attn_gqa/cuda.py:394);
+  - optional trailing positional arguments fuse RoPE and ALiBi:
+    apply(Q, K, V, causal, tau, rope_cos, rope_sin, alibi_slopes, window_left)
+    with fp32 tables [positions, D/2] (rotation at positions 0..T-1 for Q and
+    K) and fp32 slopes [Hq];
+  - any T (the reference requires T to be a multiple of its block size).
+The forward saves O and the log-sum-exp M (natural log, fp32 [B, H, T]) like
+the reference (:571-575).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+
+
+class _FlashAttentionBase(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, K, V, causal, tau, rope_cos=None, rope_sin=None, alibi_slopes=None, window_left=-1):  # noqa: N803
+        if Q.dim() != 4 or K.dim() != 4 or V.dim() != 4:
+            raise ValueError("Q, K, V must be [B, H, T, D]")
+        rope = rope_cos is not None
+        o, lse = ops.attention_prefill(
+            Q.transpose(1, 2),
+            K.transpose(1, 2),
+            V.transpose(1, 2),
+            causal=bool(causal),
+            softmax_scale=float(tau),
+            window_left=int(window_left),
+            alibi_slopes=alibi_slopes,
+            rope_cos=rope_cos,
+            rope_sin=rope_sin,
+            rope_q=rope,
+            rope_k=rope,
+            return_lse=True,
+        )
+        O = o.transpose(1, 2)  # noqa: N806  [B, H, T, D] view of a [B, T, H, D] buffer
+        ctx.save_for_backward(Q, K, V, O, lse)
+        ctx.causal = bool(causal)
+        ctx.tau = float(tau)
+        ctx.window_left = int(window_left)
+        ctx.has_extras = rope or alibi_slopes is not None
+        return O
+
+    @staticmethod
+    def backward(ctx, dO):  # noqa: N803
+        raise NotImplementedError(
+            "goda_amd: the HIP backward kernels are not built yet; use the forward in no_grad/eval"
+        )
+
+
+class FlashAttentionGQAKernel(_FlashAttentionBase):
+    """kernels_/flash_attn_gqa/cuda.py:510-658 — same call, real GQA."""
+
+
+class FlashAttentionMQAKernel(_FlashAttentionBase):
+    """kernels_/flash_attn_mqa/cuda.py:468-610 — same call, real MQA (Hkv = 1)."""
+
+
+__all__ = ["FlashAttentionGQAKernel", "FlashAttentionMQAKernel"]

@@ -1,0 +1,349 @@
+"""Torch-facing entry points of the HIP attention library.
+
+All tensors must live on the GPU; outputs and workspaces are allocated with
+PyTorch's caching allocator and every launch goes on
+`torch.cuda.current_stream()`. There is no CPU path: calling these with CPU
+tensors raises.
+
+Layouts (any strides, last dim contiguous):
+  dense   q [B, Tq, Hq, D], k/v [B, Tk, Hkv, D]
+  varlen  q [total_q, Hq, D], k/v [total_k, Hkv, D] with int32 cu_seqlens
+The reference's kernel layout [B, H, T, D] is passed as `x.transpose(1, 2)`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.float32: _lib.DTYPE_F32,
+    torch.float16: _lib.DTYPE_F16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require_gpu(name: str, t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"goda_amd: {name} must be a GPU tensor (got {t.device})")
+
+
+def _require_last_contig(name: str, t: torch.Tensor) -> None:
+    if t.stride(-1) != 1:
+        raise ValueError(f"goda_amd: {name} must be contiguous in its last dimension")
+
+
+def _i32_vec(name: str, t: torch.Tensor | None, n: int, device: torch.device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or t.dim() != 1 or t.numel() != n:
+        raise ValueError(f"goda_amd: {name} must be an int32 vector of length {n}")
+    if t.device != device:
+        raise ValueError(f"goda_amd: {name} must be on {device}")
+    return t.contiguous()
+
+
+def _f32_vec(name: str, t: torch.Tensor | None, n: int, device: torch.device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    t = t.reshape(-1)
+    if t.numel() != n:
+        raise ValueError(f"goda_amd: {name} must have {n} elements")
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+def _rope_tables(cos: torch.Tensor | None, sin: torch.Tensor | None, head_dim: int, device):
+    if cos is None and sin is None:
+        return None, None, 0
+    if cos is None or sin is None:
+        raise ValueError("goda_amd: rope_cos and rope_sin go together")
+    cos = cos.reshape(-1, head_dim // 2).to(device=device, dtype=torch.float32).contiguous()
+    sin = sin.reshape(-1, head_dim // 2).to(device=device, dtype=torch.float32).contiguous()
+    if cos.shape != sin.shape:
+        raise ValueError("goda_amd: rope_cos and rope_sin shapes differ")
+    return cos, sin, cos.shape[0]
+
+
+def attention_prefill(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    causal: bool,
+    softmax_scale: float | None = None,
+    window_left: int = -1,
+    alibi_slopes: torch.Tensor | None = None,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    rope_q: bool = False,
+    rope_k: bool = False,
+    rope_q_offset: int = 0,
+    rope_k_offset: int = 0,
+    cu_seqlens_q: torch.Tensor | None = None,
+    cu_seqlens_k: torch.Tensor | None = None,
+    max_seqlen_q: int | None = None,
+    max_seqlen_k: int | None = None,
+    seqused_k: torch.Tensor | None = None,
+    return_lse: bool = False,
+    out: torch.Tensor | None = None,
+):
+    """Prefill attention through `goda_attn_prefill_fwd`.
+
+    Semantics are those of goda's eager path (mint/nn/flashattn.py:221-273):
+    GQA head mapping h -> h // (Hq/Hkv), bottom-right causal alignment, left
+    window only with causal (or a single query), ALiBi as
+    slope_h * (j - i_abs), RoPE as mint/nn/pos.py:155-177 using the given
+    fp32 cos/sin tables. Returns `o` (and `lse` fp32 if `return_lse`).
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_gpu(name, t)
+        _require_last_contig(name, t)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"goda_amd: q/k/v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"goda_amd: unsupported dtype {q.dtype}")
+    varlen = cu_seqlens_q is not None
+    if (cu_seqlens_k is not None) != varlen:
+        raise ValueError("goda_amd: cu_seqlens_q and cu_seqlens_k go together")
+    dev = q.device
+    if varlen:
+        if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+            raise ValueError("goda_amd: varlen q/k/v must be [total, H, D]")
+        batch = cu_seqlens_q.numel() - 1
+        cu_q = _i32_vec("cu_seqlens_q", cu_seqlens_q, batch + 1, dev)
+        cu_k = _i32_vec("cu_seqlens_k", cu_seqlens_k, batch + 1, dev)
+        if max_seqlen_q is None or max_seqlen_k is None:
+            raise ValueError("goda_amd: varlen needs max_seqlen_q and max_seqlen_k")
+        tq, tk = int(max_seqlen_q), int(max_seqlen_k)
+        hq, d = q.shape[1], q.shape[2]
+        hkv = k.shape[1]
+        qs = (0, q.stride(0), q.stride(1))
+        ks = (0, k.stride(0), k.stride(1))
+        vs = (0, v.stride(0), v.stride(1))
+        if v.shape[1] != hkv or k.shape[2] != d or v.shape[2] != d or k.shape[0] != v.shape[0]:
+            raise ValueError("goda_amd: k/v shapes do not match q")
+    else:
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+            raise ValueError("goda_amd: dense q/k/v must be [B, T, H, D]")
+        batch, tq, hq, d = q.shape
+        _, tk, hkv, _ = k.shape
+        if k.shape[0] != batch or v.shape != k.shape or k.shape[3] != d:
+            raise ValueError(f"goda_amd: k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
+        cu_q = cu_k = None
+        qs = (q.stride(0), q.stride(1), q.stride(2))
+        ks = (k.stride(0), k.stride(1), k.stride(2))
+        vs = (v.stride(0), v.stride(1), v.stride(2))
+    if hq % hkv != 0:
+        raise ValueError(f"goda_amd: heads_q {hq} is not a multiple of heads_kv {hkv}")
+    used = _i32_vec("seqused_k", seqused_k, batch, dev)
+
+    if out is None:
+        o = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    else:
+        if out.shape != q.shape or out.dtype != q.dtype or out.device != dev:
+            raise ValueError("goda_amd: out must match q's shape, dtype and device")
+        _require_last_contig("out", out)
+        o = out
+    os_ = (0, o.stride(0), o.stride(1)) if varlen else (o.stride(0), o.stride(1), o.stride(2))
+
+    lse = None
+    if return_lse:
+        lse = torch.empty((hq, q.shape[0]) if varlen else (batch, hq, tq), dtype=torch.float32, device=dev)
+
+    slopes = _f32_vec("alibi_slopes", alibi_slopes, hq, dev)
+    cos, sin, rope_len = _rope_tables(rope_cos, rope_sin, d, dev)
+    if (rope_q or rope_k) and cos is None:
+        raise ValueError("goda_amd: rope_q/rope_k need rope_cos and rope_sin")
+
+    a = _lib.PrefillArgs()
+    a.dtype = _DTYPES[q.dtype]
+    a.batch, a.heads_q, a.heads_kv, a.head_dim = batch, hq, hkv, d
+    a.seqlen_q, a.seqlen_k = tq, tk
+    a.causal = int(bool(causal))
+    a.window_left = int(window_left)
+    a.softmax_scale = float(softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d))
+    a.q, a.k, a.v, a.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = qs
+    a.k_stride_b, a.k_stride_t, a.k_stride_h = ks
+    a.v_stride_b, a.v_stride_t, a.v_stride_h = vs
+    a.o_stride_b, a.o_stride_t, a.o_stride_h = os_
+    if lse is not None:
+        a.lse = lse.data_ptr()
+        if varlen:
+            a.lse_stride_b, a.lse_stride_h = 0, lse.stride(0)
+        else:
+            a.lse_stride_b, a.lse_stride_h = lse.stride(0), lse.stride(1)
+    a.cu_seqlens_q, a.cu_seqlens_k = _ptr(cu_q), _ptr(cu_k)
+    a.seqused_k = _ptr(used)
+    a.alibi_slopes = _ptr(slopes)
+    a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
+    a.rope_q, a.rope_k = int(bool(rope_q)), int(bool(rope_k))
+    a.rope_q_offset, a.rope_k_offset = int(rope_q_offset), int(rope_k_offset)
+
+    lib = _lib.load()
+    need = lib.goda_attn_prefill_workspace_size(ctypes.byref(a))
+    if need < 0:
+        _lib.check(int(need))
+    ws = None
+    if need > 0:
+        ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
+    # Temporaries (ws, slopes, tables) are freed after the launch is enqueued;
+    # the caching allocator only reuses them for work ordered after it on
+    # this stream.
+    _lib.check(lib.goda_attn_prefill_fwd(ctypes.byref(a), _stream()))
+    return (o, lse) if return_lse else o
+
+
+def attention_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    *,
+    softmax_scale: float | None = None,
+    window_left: int = -1,
+    alibi_slopes: torch.Tensor | None = None,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    rope_q: bool = False,
+    rope_q_offset: int = 0,
+    split_size: int = 0,
+    cache_layout: str = "bthd",
+    return_lse: bool = False,
+    out: torch.Tensor | None = None,
+):
+    """One-token decode over a KV cache with per-sequence lengths.
+
+    q: [B, Hq, D] (or [B, 1, Hq, D]); caches [B, Lmax, Hkv, D] when
+    cache_layout == "bthd" (goda's KVCache, mint/kvcache/base.py:22-31) or
+    [B, Hkv, Lmax, D] when "bhtd"; cache_seqlens int32 [B] = valid keys
+    (the new token included). The query sits at position cache_seqlens[b]-1.
+    """
+    squeeze = False
+    if q.dim() == 4:
+        if q.shape[1] != 1:
+            raise ValueError("goda_amd: decode takes one query token per sequence")
+        q = q[:, 0]
+        squeeze = True
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_gpu(name, t)
+        _require_last_contig(name, t)
+    if not (q.dtype == k_cache.dtype == v_cache.dtype) or q.dtype not in _DTYPES:
+        raise ValueError("goda_amd: q and caches must share a supported dtype")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("goda_amd: k_cache and v_cache shapes differ")
+    b, hq, d = q.shape
+    if cache_layout == "bthd":
+        _, lmax, hkv, dk = k_cache.shape
+        ks = (k_cache.stride(0), k_cache.stride(1), k_cache.stride(2))
+        vs = (v_cache.stride(0), v_cache.stride(1), v_cache.stride(2))
+    elif cache_layout == "bhtd":
+        _, hkv, lmax, dk = k_cache.shape
+        ks = (k_cache.stride(0), k_cache.stride(2), k_cache.stride(1))
+        vs = (v_cache.stride(0), v_cache.stride(2), v_cache.stride(1))
+    else:
+        raise ValueError(f"goda_amd: unknown cache_layout {cache_layout!r}")
+    if k_cache.shape[0] < b or dk != d:
+        raise ValueError("goda_amd: cache shape does not match q")
+    if hq % hkv != 0:
+        raise ValueError(f"goda_amd: heads_q {hq} is not a multiple of heads_kv {hkv}")
+    dev = q.device
+    seqlens = _i32_vec("cache_seqlens", cache_seqlens[:b] if cache_seqlens.numel() > b else cache_seqlens, b, dev)
+    o = torch.empty_like(q) if out is None else out
+    lse = torch.empty((b, hq), dtype=torch.float32, device=dev) if return_lse else None
+    slopes = _f32_vec("alibi_slopes", alibi_slopes, hq, dev)
+    cos, sin, rope_len = _rope_tables(rope_cos, rope_sin, d, dev)
+    if rope_q and cos is None:
+        raise ValueError("goda_amd: rope_q needs rope_cos and rope_sin")
+
+    a = _lib.DecodeArgs()
+    a.dtype = _DTYPES[q.dtype]
+    a.batch, a.heads_q, a.heads_kv, a.head_dim = b, hq, hkv, d
+    a.max_seqlen = lmax
+    a.window_left = int(window_left)
+    a.split_size = int(split_size)
+    a.softmax_scale = float(softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d))
+    a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k_cache = k_cache.data_ptr()
+    a.k_stride_b, a.k_stride_t, a.k_stride_h = ks
+    a.v_cache = v_cache.data_ptr()
+    a.v_stride_b, a.v_stride_t, a.v_stride_h = vs
+    a.cache_seqlens = seqlens.data_ptr()
+    a.o, a.o_stride_b, a.o_stride_h = o.data_ptr(), o.stride(0), o.stride(1)
+    if lse is not None:
+        a.lse, a.lse_stride_b = lse.data_ptr(), lse.stride(0)
+    a.alibi_slopes = _ptr(slopes)
+    a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
+    a.rope_q, a.rope_q_offset = int(bool(rope_q)), int(rope_q_offset)
+
+    lib = _lib.load()
+    need = lib.goda_attn_decode_workspace_size(ctypes.byref(a))
+    if need < 0:
+        _lib.check(int(need))
+    ws = None
+    if need > 0:
+        ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
+    _lib.check(lib.goda_attn_decode(ctypes.byref(a), _stream()))
+    if squeeze:
+        o = o.unsqueeze(1)
+    return (o, lse) if return_lse else o
+
+
+def kv_append(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    *,
+    rope_cos: torch.Tensor | None = None,
+    rope_sin: torch.Tensor | None = None,
+    rope_k: bool = False,
+    rope_k_offset: int = 0,
+) -> None:
+    """Write k_new/v_new [B, Tn, Hkv, D] into caches [Bmax, Lmax, Hkv, D] at
+    each sequence's own position cache_seqlens[b], then advance the lengths —
+    all on the device, with no host read of the lengths."""
+    for name, t in (("k_new", k_new), ("v_new", v_new), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_gpu(name, t)
+        _require_last_contig(name, t)
+    if not (k_new.dtype == v_new.dtype == k_cache.dtype == v_cache.dtype) or k_new.dtype not in _DTYPES:
+        raise ValueError("goda_amd: kv_append tensors must share a supported dtype")
+    b, tn, hkv, d = k_new.shape
+    if v_new.shape != k_new.shape or k_cache.shape[2:] != (hkv, d) or k_cache.shape != v_cache.shape:
+        raise ValueError("goda_amd: kv_append shapes do not match")
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.numel() < b or not cache_seqlens.is_contiguous():
+        raise ValueError("goda_amd: cache_seqlens must be a contiguous int32 vector")
+    dev = k_new.device
+    cos, sin, rope_len = _rope_tables(rope_cos, rope_sin, d, dev)
+    if rope_k and cos is None:
+        raise ValueError("goda_amd: rope_k needs rope_cos and rope_sin")
+    a = _lib.KvAppendArgs()
+    a.dtype = _DTYPES[k_new.dtype]
+    a.batch, a.heads_kv, a.head_dim = b, hkv, d
+    a.max_seqlen, a.seqlen_new = k_cache.shape[1], tn
+    a.k_new, a.v_new = k_new.data_ptr(), v_new.data_ptr()
+    a.kn_stride_b, a.kn_stride_t, a.kn_stride_h = k_new.stride(0), k_new.stride(1), k_new.stride(2)
+    a.vn_stride_b, a.vn_stride_t, a.vn_stride_h = v_new.stride(0), v_new.stride(1), v_new.stride(2)
+    a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    a.k_stride_b, a.k_stride_t, a.k_stride_h = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v_stride_b, a.v_stride_t, a.v_stride_h = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    a.cache_seqlens = cache_seqlens.data_ptr()
+    a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
+    a.rope_k, a.rope_k_offset = int(bool(rope_k)), int(rope_k_offset)
+    _lib.check(_lib.load().goda_attn_kv_append(ctypes.byref(a), _stream()))
+

@@ -1,0 +1,189 @@
+"""The five benchmark / parity workloads of the attention hot path, with
+seeded synthetic inputs and their algorithmic work counts.
+
+  cfg1  d12 causal GQA fp32, B=2, T=512, Hq=6, Hkv=2, D=128, RoPE 10000
+  cfg2  causal GQA prefill bf16, B=4, T=8192, Hq=32, Hkv=8, D=128, RoPE 10000
+  cfg3  causal MQA prefill bf16, B=8, T=4096, Hq=16, Hkv=1, D=256, ALiBi
+  cfg4  decode bf16, B=64, Hq=32, Hkv=8, D=128, cache [64, 8, 32768, 128],
+        per-sequence lengths uniform in [1024, 32768]
+  cfg5  ragged mix bf16, Hq=8, Hkv=1, D=256, RoPE 10000: 16 packed prefill
+        sequences T ~ U[128, 4096] + 48 decode sequences L ~ U[512, 16384]
+
+Inputs are N(0, 1) * 0.5 drawn in fp32 from a seeded generator and cast to the
+workload dtype (cfg1: fp32, std 1). Lengths come from the same seed. Large
+tensors are drawn on the target device with a device generator, so CPU
+checkers copy the exact bytes back.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 flop/clk x 2.4 GHz)
+FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBPS = 8000.0
+
+
+@dataclass
+class Prefill:
+    name: str
+    dtype: torch.dtype
+    batch: int
+    seqlen: int
+    heads_q: int
+    heads_kv: int
+    head_dim: int
+    causal: bool = True
+    rope_base: float | None = 10000.0
+    alibi: bool = False
+    std: float = 0.5
+    seed: int = 0
+    lengths: tuple[int, int] | None = None  # varlen: uniform [lo, hi] per sequence
+
+
+@dataclass
+class Decode:
+    name: str
+    dtype: torch.dtype
+    batch: int
+    heads_q: int
+    heads_kv: int
+    head_dim: int
+    max_seqlen: int
+    lengths: tuple[int, int]
+    rope_base: float | None = None
+    std: float = 0.5
+    seed: int = 0
+    cache_layout: str = "bhtd"
+
+
+@dataclass
+class Mix:
+    name: str
+    prefill: Prefill
+    decode: Decode
+    extra: dict = field(default_factory=dict)
+
+
+CFG1 = Prefill("cfg1_d12_gqa_fp32", torch.float32, 2, 512, 6, 2, 128, std=1.0, seed=101)
+CFG2 = Prefill("cfg2_gqa_prefill_bf16", torch.bfloat16, 4, 8192, 32, 8, 128, seed=202)
+CFG3 = Prefill("cfg3_mqa_alibi_bf16", torch.bfloat16, 8, 4096, 16, 1, 256, rope_base=None, alibi=True, seed=303)
+CFG4 = Decode("cfg4_decode_bf16", torch.bfloat16, 64, 32, 8, 128, 32768, (1024, 32768), seed=404)
+CFG5 = Mix(
+    "cfg5_mix_bf16",
+    Prefill("cfg5_prefill", torch.bfloat16, 16, 4096, 8, 1, 256, seed=505, lengths=(128, 4096)),
+    Decode("cfg5_decode", torch.bfloat16, 48, 8, 1, 256, 16384, (512, 16384), rope_base=10000.0, seed=506),
+)
+
+ALL = {c.name: c for c in (CFG1, CFG2, CFG3, CFG4, CFG5)}
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def _randn(shape, std, dtype, device, gen):
+    return (torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+
+def rope_tables(seq_len: int, head_dim: int, base: float, device="cpu", scale_factor: float = 1.0):
+    """fp32 cos/sin [seq_len, head_dim/2] computed as goda's RoPE buffers
+    (mint/nn/pos.py:136-153; LinearScaledRoPE divides t, :192-213)."""
+    channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
+    inv_freq = 1.0 / (base ** (channel_range / head_dim))
+    t = torch.arange(seq_len, dtype=torch.float32)
+    if scale_factor != 1.0:
+        t = t / scale_factor
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos().to(device), freqs.sin().to(device)
+
+
+def alibi_slopes(n_heads: int) -> list[float]:
+    """goda's ALiBi slopes (mint/nn/pos.py:236-249)."""
+
+    def pow2(n: int) -> list[float]:
+        start = 2 ** (-(2 ** -(math.log2(n) - 3)))
+        return [start * (start**i) for i in range(n)]
+
+    if math.log2(n_heads).is_integer():
+        return pow2(n_heads)
+    closest = 2 ** math.floor(math.log2(n_heads))
+    return pow2(closest) + alibi_slopes(2 * closest)[0::2][: n_heads - closest]
+
+
+def seq_lengths(lo: int, hi: int, n: int, seed: int) -> torch.Tensor:
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return torch.randint(lo, hi + 1, (n,), generator=g, dtype=torch.int64).to(torch.int32)
+
+
+def prefill_inputs(w: Prefill, device="cuda") -> dict:
+    """q/k/v in goda's module layout [B, T, H, D] (dense) or packed
+    [Σ T, H, D] with cu_seqlens (varlen)."""
+    gen = _gen(device, w.seed)
+    out: dict = {}
+    if w.lengths is not None:
+        lens = seq_lengths(w.lengths[0], w.lengths[1], w.batch, w.seed + 1)
+        cu = torch.zeros(w.batch + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(lens, 0)
+        total = int(cu[-1])
+        out["lengths"] = lens
+        out["cu_seqlens"] = cu.to(device)
+        out["max_seqlen"] = int(lens.max())
+        shape_q = (total, w.heads_q, w.head_dim)
+        shape_k = (total, w.heads_kv, w.head_dim)
+    else:
+        shape_q = (w.batch, w.seqlen, w.heads_q, w.head_dim)
+        shape_k = (w.batch, w.seqlen, w.heads_kv, w.head_dim)
+    out["q"] = _randn(shape_q, w.std, w.dtype, device, gen)
+    out["k"] = _randn(shape_k, w.std, w.dtype, device, gen)
+    out["v"] = _randn(shape_k, w.std, w.dtype, device, gen)
+    if w.rope_base is not None:
+        out["rope_cos"], out["rope_sin"] = rope_tables(w.seqlen, w.head_dim, w.rope_base, device)
+    if w.alibi:
+        out["alibi_slopes"] = torch.tensor(alibi_slopes(w.heads_q), dtype=torch.float32, device=device)
+    return out
+
+
+def decode_inputs(w: Decode, device="cuda") -> dict:
+    """q [B, Hq, D]; caches in `w.cache_layout` ("bhtd": [B, Hkv, Lmax, D])."""
+    gen = _gen(device, w.seed)
+    lens = seq_lengths(w.lengths[0], w.lengths[1], w.batch, w.seed + 1)
+    if w.cache_layout == "bhtd":
+        shape = (w.batch, w.heads_kv, w.max_seqlen, w.head_dim)
+    else:
+        shape = (w.batch, w.max_seqlen, w.heads_kv, w.head_dim)
+    out = {
+        "q": _randn((w.batch, w.heads_q, w.head_dim), w.std, w.dtype, device, gen),
+        "k_cache": _randn(shape, w.std, w.dtype, device, gen),
+        "v_cache": _randn(shape, w.std, w.dtype, device, gen),
+        "lengths": lens,
+        "cache_seqlens": lens.to(device),
+    }
+    if w.rope_base is not None:
+        out["rope_cos"], out["rope_sin"] = rope_tables(w.max_seqlen, w.head_dim, w.rope_base, device)
+    return out
+
+
+def prefill_flops(w: Prefill, lengths: torch.Tensor | None = None) -> float:
+    """Algorithmic FLOPs of QK^T and PV over visible pairs:
+    4 * D * Hq * Σ_b T_b (T_b + 1) / 2 for causal, 4 * D * Hq * Σ T_b^2 otherwise."""
+    if lengths is None:
+        lengths = torch.full((w.batch,), w.seqlen, dtype=torch.int64)
+    t = lengths.to(torch.float64)
+    pairs = (t * (t + 1) / 2).sum() if w.causal else (t * t).sum()
+    return float(4.0 * w.head_dim * w.heads_q * pairs)
+
+
+def decode_bytes(w: Decode, lengths: torch.Tensor) -> float:
+    """Algorithmic HBM bytes of one decode step: each valid cached K and V
+    element once (shared by the query-head group), plus q in and o out."""
+    es = torch.finfo(w.dtype).bits // 8
+    kv = float(lengths.to(torch.float64).sum()) * w.heads_kv * w.head_dim * 2 * es
+    qo = w.batch * w.heads_q * w.head_dim * 2 * es
+    return kv + qo

@@ -1,0 +1,209 @@
+/*
+ * goda_attn.h -- C-ABI of the MI355X (gfx950) attention hot path.
+ *
+ * The library (libgoda_attn.so) replaces the attention kernels that goda calls
+ * from Python. Every entry point takes plain device pointers, element strides
+ * and sizes; nothing here names a framework type. Work is enqueued on the HIP
+ * stream passed in `stream` (a hipStream_t; NULL = the default stream) and the
+ * call returns without synchronising. The library never allocates device
+ * memory: outputs and the workspace are owned by the caller.
+ *
+ * Logical layouts (strides are in ELEMENTS, the head dimension must be
+ * contiguous, i.e. stride 1):
+ *   dense  q/o : [batch, seqlen_q, heads_q,  head_dim]   any (b, t, h) strides
+ *   dense  k/v : [batch, seqlen_k, heads_kv, head_dim]   any (b, t, h) strides
+ *   varlen q/o : [total_q, heads_q,  head_dim], rows of sequence b are
+ *                cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1  (stride_b ignored)
+ *   varlen k/v : same with cu_seqlens_k
+ * so both goda's module layout [B,T,H,D] (mint/nn/attn.py:53-55) and the kernel
+ * layout [B,H,T,D] (kernels_/flash_attn_gqa/cuda.py:358-363) are accepted as
+ * strided views without copies.
+ *
+ * Semantics follow goda's eager attention (mint/nn/flashattn.py:221-273):
+ *   - query head h reads key/value head h / (heads_q / heads_kv);
+ *   - causal alignment is bottom-right: query row i of a sequence with Lq
+ *     queries and Lk keys sees key j iff j <= (Lk - Lq) + i;
+ *   - left window W >= 0 additionally requires (Lk - Lq + i) - j <= W;
+ *   - ALiBi adds slope[h] * (j - (Lk - Lq + i)) to the scaled score
+ *     (mint/nn/pos.py:251-272);
+ *   - RoPE is the half-split rotation of mint/nn/pos.py:155-163 with caller
+ *     supplied fp32 cos/sin tables [rope_len, head_dim/2]; query row i is
+ *     rotated at position rope_q_offset + (Lk - Lq) + i, key row j at
+ *     rope_k_offset + j;
+ *   - lse = ln(sum_j exp(score_ij)) over the scaled, biased, unmasked scores
+ *     (kernels_/flash_attn_gqa/cuda.py:496-499). A row with no visible key
+ *     produces o = 0 and lse = -inf.
+ *
+ * Every entry point returns GODA_OK (0) or a negative status; the message of
+ * the last failure on the calling thread is returned by goda_attn_last_error.
+ */
+#ifndef GODA_ATTN_H
+#define GODA_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GODA_ATTN_ABI_VERSION 1
+
+/* element types */
+#define GODA_DTYPE_F32 0
+#define GODA_DTYPE_F16 1
+#define GODA_DTYPE_BF16 2
+
+/* status codes */
+#define GODA_OK 0
+#define GODA_ERR_INVALID_ARG (-1)
+#define GODA_ERR_UNSUPPORTED (-2)
+#define GODA_ERR_WORKSPACE (-3)
+#define GODA_ERR_HIP (-4)
+
+typedef struct goda_prefill_args {
+  int32_t dtype;       /* GODA_DTYPE_* of q, k, v and o */
+  int32_t batch;       /* number of sequences */
+  int32_t heads_q;
+  int32_t heads_kv;    /* must divide heads_q */
+  int32_t head_dim;
+  int32_t seqlen_q;    /* dense: T_q; varlen: max over sequences */
+  int32_t seqlen_k;    /* dense: T_k; varlen: max over sequences */
+  int32_t causal;      /* 0 / 1 */
+  int32_t window_left; /* -1: unlimited */
+  float softmax_scale; /* goda uses 1/sqrt(head_dim) (mint/nn/flashattn.py:143) */
+
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_stride_b, q_stride_t, q_stride_h;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  int64_t o_stride_b, o_stride_t, o_stride_h;
+
+  /* fp32 log-sum-exp, dense [B, Hq, T_q] / varlen [Hq, total_q]; row stride 1.
+   * NULL: not written. */
+  float* lse;
+  int64_t lse_stride_b, lse_stride_h;
+
+  const int32_t* cu_seqlens_q; /* [batch+1] or NULL (dense) */
+  const int32_t* cu_seqlens_k; /* [batch+1] or NULL (dense) */
+  const int32_t* seqused_k;    /* [batch] keys used per sequence, or NULL */
+
+  const float* alibi_slopes;   /* [heads_q] or NULL */
+
+  const float* rope_cos;       /* [rope_len, head_dim/2] fp32, or NULL */
+  const float* rope_sin;
+  int32_t rope_len;
+  int32_t rope_q;              /* rotate q rows */
+  int32_t rope_k;              /* rotate k rows */
+  int32_t rope_q_offset;
+  int32_t rope_k_offset;
+  int32_t reserved0;
+
+  void* workspace;             /* size from goda_attn_prefill_workspace_size */
+  int64_t workspace_bytes;
+} goda_prefill_args;
+
+typedef struct goda_decode_args {
+  int32_t dtype;
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t head_dim;
+  int32_t max_seqlen;   /* rows of the cache (Lmax) */
+  int32_t window_left;  /* -1: unlimited */
+  int32_t split_size;   /* keys per split-K chunk; 0 = library default */
+  float softmax_scale;
+  int32_t reserved0;
+
+  const void* q;        /* [batch, heads_q, head_dim]: one new token per sequence */
+  int64_t q_stride_b, q_stride_h;
+  const void* k_cache;  /* [batch, Lmax, heads_kv, D] or [batch, heads_kv, Lmax, D] via strides */
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  const void* v_cache;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  const int32_t* cache_seqlens; /* [batch] valid keys per sequence (new token included) */
+  void* o;              /* [batch, heads_q, head_dim] */
+  int64_t o_stride_b, o_stride_h;
+  float* lse;           /* [batch, heads_q] fp32 or NULL */
+  int64_t lse_stride_b;
+
+  const float* alibi_slopes; /* [heads_q] or NULL */
+  const float* rope_cos;     /* rotate q at position cache_seqlens[b]-1+rope_q_offset */
+  const float* rope_sin;
+  int32_t rope_len;
+  int32_t rope_q;
+  int32_t rope_q_offset;
+  int32_t reserved1;
+
+  void* workspace;           /* size from goda_attn_decode_workspace_size */
+  int64_t workspace_bytes;
+} goda_decode_args;
+
+typedef struct goda_kv_append_args {
+  int32_t dtype;
+  int32_t batch;
+  int32_t heads_kv;
+  int32_t head_dim;
+  int32_t max_seqlen;   /* rows of the cache (Lmax) */
+  int32_t seqlen_new;   /* rows appended to every sequence */
+  const void* k_new;    /* [batch, seqlen_new, heads_kv, D] via strides */
+  int64_t kn_stride_b, kn_stride_t, kn_stride_h;
+  const void* v_new;
+  int64_t vn_stride_b, vn_stride_t, vn_stride_h;
+  void* k_cache;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  void* v_cache;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  int32_t* cache_seqlens; /* [batch]: in = write position, out = position + seqlen_new */
+  const float* rope_cos;  /* rotate new k rows at their cache position + rope_k_offset */
+  const float* rope_sin;
+  int32_t rope_len;
+  int32_t rope_k;
+  int32_t rope_k_offset;
+  int32_t reserved0;
+} goda_kv_append_args;
+
+/* ABI version and struct sizes, so that a binding can check its mirror. */
+int32_t goda_attn_abi_version(void);
+int64_t goda_attn_sizeof_prefill_args(void);
+int64_t goda_attn_sizeof_decode_args(void);
+int64_t goda_attn_sizeof_kv_append_args(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* goda_attn_last_error(void);
+
+/* Workspace needed by goda_attn_prefill_fwd for these arguments (bytes, >= 0),
+ * or a negative status if the arguments are rejected. */
+int64_t goda_attn_prefill_workspace_size(const goda_prefill_args* args);
+
+/* Causal / non-causal GQA-MQA prefill forward: o = softmax(q k^T * scale + bias) v,
+ * plus the optional lse. Replaces FlashAttentionGQAKernel.forward
+ * (kernels_/flash_attn_gqa/cuda.py:515-575), FlashAttentionMQAKernel.forward
+ * (kernels_/flash_attn_mqa/cuda.py:470-527) and the SDPA branch of
+ * FlashAttention._attention (mint/nn/flashattn.py:156-172, 221-273), including
+ * the packed varlen call of mint/nn/flashattn.py:123-133 (cu_seqlens). */
+int32_t goda_attn_prefill_fwd(const goda_prefill_args* args, void* stream);
+
+/* Workspace needed by goda_attn_decode for these arguments (bytes, >= 0). */
+int64_t goda_attn_decode_workspace_size(const goda_decode_args* args);
+
+/* One-token decode over a contiguous KV cache with per-sequence lengths:
+ * split-K partial softmax over chunks of the cache, merged by log-sum-exp.
+ * Replaces FlashAttention._attention_with_kvcache for q_len == 1
+ * (mint/nn/flashattn.py:174-219); its argument set mirrors the
+ * flash_attn_with_kvcache call at mint/nn/flashattn.py:191-200. */
+int32_t goda_attn_decode(const goda_decode_args* args, void* stream);
+
+/* Append seqlen_new rows of k/v to every sequence at its own position
+ * cache_seqlens[b] (optionally rotating k), then advance cache_seqlens.
+ * Replaces KVCache.update (mint/kvcache/base.py:35-50) without the
+ * device-to-host read of mint/nn/flashattn.py:202. */
+int32_t goda_attn_kv_append(const goda_kv_append_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GODA_ATTN_H */

@@ -1,0 +1,91 @@
+"""Float64 brute-force attention with explicit loops (numpy) — TEST
+INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Independent of torch's SDPA: scores, masks, biases and the softmax are written
+out per query row, so a mistake in oracle/attention.py's use of SDPA (mask
+polarity, GQA head mapping, bias sign, window edge) shows up as a mismatch.
+Small shapes only.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def attention(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    *,
+    causal: bool,
+    window_left: int = -1,
+    slopes: np.ndarray | None = None,
+    doc_ids: np.ndarray | None = None,
+    scale: float | None = None,
+):
+    """q [B, Tq, Hq, D], k/v [B, Tk, Hkv, D] -> (o [B, Tq, Hq, D], lse [B, Hq, Tq]).
+
+    Query row i of Tq sits at absolute position i_abs = Tk - Tq + i; key j is
+    visible iff (not causal or j <= i_abs) and (window: i_abs - j <= W, with
+    causal or Tq == 1) and (doc ids equal). Bias slope_h * (j - i_abs).
+    A row with no visible key gives o = 0, lse = -inf.
+    """
+    q = q.astype(np.float64)
+    k = k.astype(np.float64)
+    v = v.astype(np.float64)
+    b_, tq, hq, d = q.shape
+    tk, hkv = k.shape[1], k.shape[2]
+    group = hq // hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    o = np.zeros((b_, tq, hq, d))
+    lse = np.full((b_, hq, tq), -np.inf)
+    for b in range(b_):
+        for h in range(hq):
+            hk = h // group
+            for i in range(tq):
+                iabs = tk - tq + i
+                logits = []
+                idx = []
+                for j in range(tk):
+                    if causal and j > iabs:
+                        continue
+                    if window_left >= 0 and (causal or tq == 1) and iabs - j > window_left:
+                        continue
+                    if doc_ids is not None and doc_ids[b, i] != doc_ids[b, j]:
+                        continue
+                    s = float(np.dot(q[b, i, h], k[b, j, hk])) * scale
+                    if slopes is not None:
+                        s += float(slopes[h]) * (j - iabs)
+                    logits.append(s)
+                    idx.append(j)
+                if not idx:
+                    continue
+                m = max(logits)
+                w = [math.exp(x - m) for x in logits]
+                z = sum(w)
+                acc = np.zeros(d)
+                for wj, j in zip(w, idx):
+                    acc += wj * v[b, j, hk]
+                o[b, i, h] = acc / z
+                lse[b, h, i] = m + math.log(z)
+    return o, lse
+
+
+def rope(x: np.ndarray, positions: np.ndarray, base: float, scale_factor: float = 1.0) -> np.ndarray:
+    """Half-split RoPE computed per element in float64 from the angle
+    definition theta_{p,i} = (p / scale_factor) * base^(-2i/D)."""
+    x = x.astype(np.float64)
+    d = x.shape[-1]
+    half = d // 2
+    out = np.empty_like(x)
+    for t, p in enumerate(positions):
+        for i in range(half):
+            theta = (p / scale_factor) * base ** (-(2.0 * i) / d)
+            c, s = math.cos(theta), math.sin(theta)
+            x1 = x[..., t, :, i]
+            x2 = x[..., t, :, i + half]
+            out[..., t, :, i] = x1 * c - x2 * s
+            out[..., t, :, i + half] = x1 * s + x2 * c
+    return out

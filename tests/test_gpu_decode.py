@@ -1,0 +1,190 @@
+"""Decode and KV-append parity: HIP path (through the C-ABI) vs the CPU oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from goda_amd import ops
+from goda_amd import workloads as wl
+from oracle import attention as ref
+from tests.helpers import TOL, lse_err, max_err, rope_oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _rand(shape, dtype, seed, std=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+def _decode_case(b, hq, hkv, d, lmax, lens, dtype, *, split=0, window=-1, alibi=False, rope=False, layout="bthd", seed=0):
+    q = _rand((b, hq, d), dtype, seed)
+    kc = _rand((b, lmax, hkv, d), dtype, seed + 1)
+    vc = _rand((b, lmax, hkv, d), dtype, seed + 2)
+    seqlens = torch.tensor(lens, dtype=torch.int32)
+    kw = {}
+    slopes = None
+    if alibi:
+        slopes = torch.tensor(wl.alibi_slopes(hq), dtype=torch.float32)
+        kw["alibi_slopes"] = slopes.to(DEV)
+    if rope:
+        cos, sin = wl.rope_tables(lmax, d, 10000.0)
+        kw.update(rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_q=True)
+    if layout == "bhtd":
+        kg = kc.transpose(1, 2).contiguous().to(DEV)
+        vg = vc.transpose(1, 2).contiguous().to(DEV)
+    else:
+        kg, vg = kc.to(DEV), vc.to(DEV)
+    o, lse = ops.attention_decode(
+        q.to(DEV), kg, vg, seqlens.to(DEV), split_size=split, window_left=window, cache_layout=layout, return_lse=True, **kw
+    )
+    torch.cuda.synchronize()
+    qr = q.float()
+    if rope:
+        # the query of sequence b sits at position seqlens[b] - 1
+        qr = torch.stack(
+            [rope_oracle(q[i][None, None], cos, sin, torch.tensor([lens[i] - 1]))[0, 0] for i in range(b)]
+        ) if min(lens) > 0 else qr
+    o_ref, lse_ref = ref.decode_attention(qr, kc.float(), vc.float(), seqlens, window_left=window, alibi_slopes=slopes)
+    tol = TOL[dtype]
+    eo = max_err(o, o_ref)
+    el = lse_err(lse, lse_ref)
+    assert eo <= tol, f"o err {eo}"
+    assert el <= (5e-3 if dtype != torch.float32 else 1e-4), f"lse err {el}"
+    return o
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 1), (4, 4), (16, 1), (6, 2)])
+def test_decode_shapes(dtype, d, hq, hkv):
+    lens = [1, 7, 64, 65, 300, 513, 1000]
+    _decode_case(len(lens), hq, hkv, d, 1024, lens, dtype, seed=hq + d)
+
+
+@pytest.mark.parametrize("split", [64, 128, 256, 1024])
+def test_decode_split_invariance(split):
+    """Splitting changes nothing: results for every split size agree with the
+    oracle (and hence with each other)."""
+    lens = [1, 200, 700, 1500, 2048]
+    _decode_case(len(lens), 16, 4, 128, 2048, lens, torch.bfloat16, split=split, seed=split)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("window", [0, 10, 100])
+def test_decode_window(dtype, window):
+    lens = [1, 50, 300, 700]
+    _decode_case(len(lens), 8, 2, 128, 800, lens, dtype, split=128, window=window, seed=window)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_alibi_rope(dtype):
+    lens = [3, 90, 400]
+    _decode_case(len(lens), 8, 2, 128, 512, lens, dtype, split=64, alibi=True, seed=3)
+    _decode_case(len(lens), 8, 1, 256, 512, lens, dtype, split=64, rope=True, seed=4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_bhtd_layout(dtype):
+    lens = [5, 333, 1024]
+    _decode_case(len(lens), 8, 2, 128, 1024, lens, dtype, split=256, layout="bhtd", seed=9)
+
+
+def test_decode_zero_length():
+    lens = [0, 10]
+    q = _rand((2, 4, 128), torch.bfloat16, 1)
+    kc = _rand((2, 64, 2, 128), torch.bfloat16, 2)
+    o, lse = ops.attention_decode(
+        q.to(DEV), kc.to(DEV), kc.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV), return_lse=True
+    )
+    o = o.cpu()
+    assert torch.all(o[0] == 0) and torch.all(torch.isneginf(lse[0].cpu()))
+    o_ref, _ = ref.decode_attention(q[1:].float(), kc[1:].float(), kc[1:].float(), torch.tensor([10]))
+    assert max_err(o[1:], o_ref) <= 2e-2
+
+
+def test_decode_matches_prefill_last_row():
+    """A decode step with cache length L equals row L-1 of causal prefill over
+    the same L tokens (the KV-cache invariant)."""
+    b, L, hq, hkv, d = 2, 300, 8, 2, 128
+    q = _rand((b, L, hq, d), torch.bfloat16, 41)
+    k = _rand((b, L, hkv, d), torch.bfloat16, 42)
+    v = _rand((b, L, hkv, d), torch.bfloat16, 43)
+    o_pre = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+    o_dec = ops.attention_decode(
+        q[:, -1].contiguous().to(DEV), k.to(DEV), v.to(DEV), torch.full((b,), L, dtype=torch.int32, device=DEV), split_size=64
+    )
+    assert max_err(o_dec, o_pre[:, -1]) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kv_append_then_decode(dtype):
+    """kv_append writes each sequence at its own position (rotating k), with no
+    host read of the lengths; then decode sees the new tokens."""
+    b, lmax, hkv, d, hq = 3, 128, 2, 128, 8
+    cos, sin = wl.rope_tables(lmax, d, 10000.0)
+    kc = torch.zeros(b, lmax, hkv, d, dtype=dtype, device=DEV)
+    vc = torch.zeros_like(kc)
+    start = torch.tensor([0, 5, 40], dtype=torch.int32)
+    seqlens = start.clone().to(DEV)
+    oracle = ref.KVCacheOracle(b, lmax, hkv, d)
+    oracle.seqlens = start.clone()
+    # prefill the existing prefixes through the same append path
+    for step, tn in enumerate([3, 1, 1]):
+        kn = _rand((b, tn, hkv, d), dtype, 100 + step)
+        vn = _rand((b, tn, hkv, d), dtype, 200 + step)
+        ops.kv_append(kn.to(DEV), vn.to(DEV), kc, vc, seqlens, rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_k=True)
+        kr = torch.stack(
+            [rope_oracle(kn[i][None], cos, sin, torch.arange(int(oracle.seqlens[i]), int(oracle.seqlens[i]) + tn))[0] for i in range(b)]
+        )
+        oracle.append(kr, vn.float())
+    torch.cuda.synchronize()
+    assert torch.equal(seqlens.cpu(), oracle.seqlens)
+    for i in range(b):
+        L = int(oracle.seqlens[i])
+        assert max_err(kc[i, :L], oracle.k[i, :L]) <= (1e-5 if dtype == torch.float32 else 1e-2)
+        assert max_err(vc[i, :L], oracle.v[i, :L]) == 0.0
+    q = _rand((b, hq, d), dtype, 300)
+    o = ops.attention_decode(q.to(DEV), kc, vc, seqlens)
+    o_ref, _ = ref.decode_attention(q.float(), kc.cpu().float(), vc.cpu().float(), oracle.seqlens)
+    assert max_err(o, o_ref) <= TOL[dtype]
+
+
+# ---------------------------------------------------------------------------
+# BASELINE decode workloads at full size
+# ---------------------------------------------------------------------------
+def _check_decode_workload(w: wl.Decode, seqs: list[int]):
+    inp = wl.decode_inputs(w, DEV)
+    kw = {}
+    if "rope_cos" in inp:
+        kw.update(rope_cos=inp["rope_cos"], rope_sin=inp["rope_sin"], rope_q=True)
+    o, lse = ops.attention_decode(
+        inp["q"], inp["k_cache"], inp["v_cache"], inp["cache_seqlens"], cache_layout=w.cache_layout, return_lse=True, **kw
+    )
+    torch.cuda.synchronize()
+    lens = inp["lengths"]
+    for b in seqs:
+        L = int(lens[b])
+        if w.cache_layout == "bhtd":
+            kb = inp["k_cache"][b : b + 1, :, :L].transpose(1, 2).cpu().float()
+            vb = inp["v_cache"][b : b + 1, :, :L].transpose(1, 2).cpu().float()
+        else:
+            kb = inp["k_cache"][b : b + 1, :L].cpu().float()
+            vb = inp["v_cache"][b : b + 1, :L].cpu().float()
+        qb = inp["q"][b : b + 1].cpu().float()
+        if "rope_cos" in inp:
+            qb = rope_oracle(inp["q"][b][None, None], inp["rope_cos"], inp["rope_sin"], torch.tensor([L - 1]))[0]
+        o_ref, lse_ref = ref.decode_attention(qb, kb, vb, torch.tensor([L]))
+        assert max_err(o[b : b + 1], o_ref) <= TOL[w.dtype], f"{w.name} seq {b}"
+        assert lse_err(lse[b : b + 1], lse_ref) <= 5e-3
+
+
+def test_cfg4_decode_full():
+    _check_decode_workload(wl.CFG4, seqs=list(range(0, 64, 3)))
+
+
+def test_cfg5_decode_full():
+    _check_decode_workload(wl.CFG5.decode, seqs=list(range(0, 48, 2)))

@@ -1,0 +1,268 @@
+"""Prefill parity: HIP path (through the C-ABI) vs the CPU oracle."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from goda_amd import ops
+from goda_amd import workloads as wl
+from oracle import attention as ref
+from tests.helpers import TOL, lse_err, max_err, rope_oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _rand(shape, dtype, seed, std=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+def _run_case(
+    b, tq, tk, hq, hkv, d, dtype, causal, *, seed=0, window=-1, alibi=False, rope=False, layout="bthd"
+):
+    q = _rand((b, tq, hq, d), dtype, seed)
+    k = _rand((b, tk, hkv, d), dtype, seed + 1)
+    v = _rand((b, tk, hkv, d), dtype, seed + 2)
+    kw = {}
+    slopes = None
+    cos = sin = None
+    if alibi:
+        slopes = torch.tensor(wl.alibi_slopes(hq), dtype=torch.float32)
+        kw["alibi_slopes"] = slopes.to(DEV)
+    if rope:
+        cos, sin = wl.rope_tables(tk + 8, d, 10000.0)
+        kw.update(rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_q=True, rope_k=True)
+    if layout == "bhtd":
+        # the reference kernel layout [B, H, T, D], passed as strided views
+        qg = q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+        kg = k.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+        vg = v.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    else:
+        qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = ops.attention_prefill(qg, kg, vg, causal=causal, window_left=window, return_lse=True, **kw)
+    torch.cuda.synchronize()
+
+    qr, kr = q.float(), k.float()
+    if rope:
+        qr = rope_oracle(q, cos, sin, torch.arange(tk - tq, tk))
+        kr = rope_oracle(k, cos, sin, torch.arange(tk))
+    o_ref, lse_ref = ref.attention_rows(
+        qr, kr, v.float(), torch.arange(tq), causal=causal, window_left=window, alibi_slopes=slopes
+    )
+    tol = TOL[dtype]
+    eo = max_err(o, o_ref)
+    el = lse_err(lse, lse_ref)
+    assert eo <= tol, f"o max err {eo} > {tol}"
+    assert el <= max(tol, 1e-3 if dtype != torch.float32 else 1e-4) * 4, f"lse max err {el}"
+    return eo
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_head_dims(dtype, d, causal):
+    _run_case(2, 128, 128, 8, 2, d, dtype, causal, seed=d)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (8, 1), (6, 1), (12, 4), (6, 2), (16, 1)])
+def test_prefill_gqa_groups(dtype, hq, hkv):
+    _run_case(2, 96, 96, hq, hkv, 128, dtype, True, seed=hq * 10 + hkv)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("tq,tk", [(100, 100), (1, 1), (37, 150), (1, 77), (200, 333), (65, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_ragged_lengths(dtype, tq, tk, causal):
+    if tq > tk and causal:
+        pytest.skip("rows with no visible key are covered by test_prefill_empty_rows")
+    _run_case(2, tq, tk, 8, 2, 128, dtype, causal, seed=tq + tk)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("window", [0, 5, 31, 64, 200])
+def test_prefill_window(dtype, window):
+    _run_case(2, 160, 160, 8, 2, 128, dtype, True, seed=window, window=window)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 8, 2), (256, 16, 1), (64, 6, 6)])
+def test_prefill_alibi(dtype, d, hq, hkv):
+    _run_case(2, 130, 130, hq, hkv, d, dtype, True, seed=d + hq, alibi=True)
+    _run_case(1, 70, 70, hq, hkv, d, dtype, False, seed=d + hq + 1, alibi=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_prefill_rope(dtype, d):
+    _run_case(2, 120, 120, 8, 2, d, dtype, True, seed=d + 7, rope=True)
+    _run_case(1, 24, 90, 4, 1, d, dtype, True, seed=d + 8, rope=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_kernel_layout_strides(dtype):
+    _run_case(2, 130, 130, 8, 2, 128, dtype, True, seed=5, layout="bhtd")
+
+
+def test_prefill_empty_rows():
+    """Lq > Lk with causal alignment: the first Lq - Lk rows see no key and
+    give o = 0, lse = -inf (a documented convention)."""
+    b, tq, tk, hq, hkv, d = 1, 40, 16, 4, 2, 128
+    q = _rand((b, tq, hq, d), torch.bfloat16, 1)
+    k = _rand((b, tk, hkv, d), torch.bfloat16, 2)
+    v = _rand((b, tk, hkv, d), torch.bfloat16, 3)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, return_lse=True)
+    o = o.cpu().float()
+    lse = lse.cpu()
+    assert torch.all(o[:, : tq - tk] == 0)
+    assert torch.all(torch.isneginf(lse[:, :, : tq - tk]))
+    o_ref, _ = ref.attention_rows(q.float(), k.float(), v.float(), torch.arange(tq - tk, tq), causal=True)
+    assert max_err(o[:, tq - tk :], o_ref) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 8, 2), (256, 8, 1)])
+def test_prefill_varlen(dtype, d, hq, hkv):
+    lens = [1, 17, 64, 65, 130, 3]
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    total = int(cu[-1])
+    q = _rand((total, hq, d), dtype, 11)
+    k = _rand((total, hkv, d), dtype, 12)
+    v = _rand((total, hkv, d), dtype, 13)
+    o = ops.attention_prefill(
+        q.to(DEV),
+        k.to(DEV),
+        v.to(DEV),
+        causal=True,
+        cu_seqlens_q=cu.to(DEV),
+        cu_seqlens_k=cu.to(DEV),
+        max_seqlen_q=max(lens),
+        max_seqlen_k=max(lens),
+    )
+    o_ref = ref.varlen_attention(q, k, v, cu, cu, causal=True)
+    assert max_err(o, o_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_seqused_k(dtype):
+    """Per-sequence key counts from the device (chunked prefill over a cache)."""
+    b, tq, lmax, hq, hkv, d = 3, 20, 200, 8, 2, 128
+    used = torch.tensor([20, 150, 77], dtype=torch.int32)
+    q = _rand((b, tq, hq, d), dtype, 21)
+    k = _rand((b, lmax, hkv, d), dtype, 22)
+    v = _rand((b, lmax, hkv, d), dtype, 23)
+    o = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, seqused_k=used.to(DEV))
+    for i in range(b):
+        L = int(used[i])
+        o_ref, _ = ref.attention_rows(
+            q[i : i + 1].float(), k[i : i + 1, :L].float(), v[i : i + 1, :L].float(), torch.arange(tq), causal=True
+        )
+        assert max_err(o[i : i + 1], o_ref) <= TOL[dtype]
+
+
+def test_prefill_softmax_scale():
+    b, t, hq, hkv, d = 1, 64, 4, 2, 128
+    q = _rand((b, t, hq, d), torch.bfloat16, 31)
+    k = _rand((b, t, hkv, d), torch.bfloat16, 32)
+    v = _rand((b, t, hkv, d), torch.bfloat16, 33)
+    o = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, softmax_scale=0.3)
+    o_ref, _ = ref.attention_rows(q.float(), k.float(), v.float(), torch.arange(t), causal=True, scale=0.3)
+    assert max_err(o, o_ref) <= 2e-2
+
+
+def test_prefill_rejects_bad_args():
+    q = torch.zeros(1, 8, 6, 128, dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros(1, 8, 4, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        ops.attention_prefill(q, k, k, causal=True)  # 6 % 4 != 0
+    q2 = torch.zeros(1, 8, 4, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(Exception):
+        ops.attention_prefill(q2, q2, q2, causal=True)  # unsupported head_dim
+    with pytest.raises(ValueError):
+        ops.attention_prefill(q.cpu(), k.cpu(), k.cpu(), causal=True)
+
+
+# ---------------------------------------------------------------------------
+# the BASELINE workloads
+# ---------------------------------------------------------------------------
+def _sample_rows(t: int, n: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    mid = torch.randint(0, t, (n,), generator=g)
+    return torch.unique(torch.cat([torch.tensor([0, 1, 63, 64, t // 2, t - 2, t - 1]), mid]))
+
+
+def _check_prefill_workload(w: wl.Prefill, rows_per_seq: int, seqs: list[int] | None = None):
+    inp = wl.prefill_inputs(w, DEV)
+    kw = {}
+    if "rope_cos" in inp:
+        kw.update(rope_cos=inp["rope_cos"], rope_sin=inp["rope_sin"], rope_q=True, rope_k=True)
+    if "alibi_slopes" in inp:
+        kw["alibi_slopes"] = inp["alibi_slopes"]
+    if w.lengths is not None:
+        kw.update(
+            cu_seqlens_q=inp["cu_seqlens"],
+            cu_seqlens_k=inp["cu_seqlens"],
+            max_seqlen_q=inp["max_seqlen"],
+            max_seqlen_k=inp["max_seqlen"],
+        )
+    o, lse = ops.attention_prefill(inp["q"], inp["k"], inp["v"], causal=w.causal, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    tol = TOL[w.dtype]
+    slopes = inp.get("alibi_slopes")
+    slopes = slopes.cpu() if slopes is not None else None
+    worst = 0.0
+    nseq = w.batch
+    for b in seqs if seqs is not None else range(nseq):
+        if w.lengths is not None:
+            s, e = int(inp["cu_seqlens"][b]), int(inp["cu_seqlens"][b + 1])
+            qb, kb, vb = inp["q"][s:e][None], inp["k"][s:e][None], inp["v"][s:e][None]
+            ob = o[s:e][None]
+            lb = lse[:, s:e][None]
+        else:
+            qb, kb, vb = inp["q"][b : b + 1], inp["k"][b : b + 1], inp["v"][b : b + 1]
+            ob, lb = o[b : b + 1], lse[b : b + 1]
+        t = qb.shape[1]
+        rows = _sample_rows(t, rows_per_seq, w.seed + b)
+        qc, kc = qb.cpu().float(), kb.cpu().float()
+        if "rope_cos" in inp:
+            qc = rope_oracle(qb, inp["rope_cos"], inp["rope_sin"], torch.arange(t))
+            kc = rope_oracle(kb, inp["rope_cos"], inp["rope_sin"], torch.arange(t))
+        o_ref, lse_ref = ref.attention_rows(qc, kc, vb.cpu().float(), rows, causal=w.causal, alibi_slopes=slopes)
+        e_o = max_err(ob[:, rows], o_ref)
+        e_l = lse_err(lb[:, :, rows], lse_ref)
+        worst = max(worst, e_o)
+        assert e_o <= tol, f"{w.name} seq {b}: o err {e_o}"
+        assert e_l <= 5e-2 if w.dtype != torch.float32 else e_l <= 1e-4, f"{w.name} seq {b}: lse err {e_l}"
+    return worst
+
+
+def test_cfg1_d12_fp32_full():
+    """cfg1 at full size against the oracle's SDPA path (all rows)."""
+    w = wl.CFG1
+    inp = wl.prefill_inputs(w, DEV)
+    o = ops.attention_prefill(
+        inp["q"], inp["k"], inp["v"], causal=True, rope_cos=inp["rope_cos"], rope_sin=inp["rope_sin"], rope_q=True, rope_k=True
+    )
+    t = w.seqlen
+    qr = rope_oracle(inp["q"], inp["rope_cos"], inp["rope_sin"], torch.arange(t))
+    kr = rope_oracle(inp["k"], inp["rope_cos"], inp["rope_sin"], torch.arange(t))
+    o_ref = ref.attention(qr, kr, inp["v"].cpu(), causal=True)
+    assert max_err(o, o_ref) <= 1e-4
+
+
+def test_cfg2_gqa_prefill_sampled_rows():
+    _check_prefill_workload(wl.CFG2, rows_per_seq=24)
+
+
+def test_cfg3_mqa_alibi_sampled_rows():
+    _check_prefill_workload(wl.CFG3, rows_per_seq=24, seqs=[0, 3, 7])
+
+
+def test_cfg5_varlen_prefill_sampled_rows():
+    _check_prefill_workload(wl.CFG5.prefill, rows_per_seq=16)
