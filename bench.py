@@ -1,0 +1,382 @@
+"""Benchmark of the goda attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input with the
+inputs already resident in HBM:
+  headline (value)  cfg2: causal GQA prefill, bf16, B=4, T=8192, Hq=32, Hkv=8,
+                    D=128, RoPE base 10000 fused (K pre-pass + attention kernel)
+  decode            cfg4: one decode token for 64 sequences, Hq=32, Hkv=8,
+                    D=128, cache [64, 8, 32768, 128], lengths U[1024, 32768]
+  also reported     cfg3 (MQA + ALiBi, D=256) and cfg5 (ragged mix, D=256)
+
+Throughputs use algorithmic work only (causal QK^T + PV flops over visible
+pairs; each valid cached K/V byte once plus q and o). The `roofline` objects
+time the dominant kernel alone with HIP events that the library records on
+its own stream around that kernel. The CPU baseline times the oracle (the
+restatement of goda's eager SDPA path, RoPE included) in the config dtype on
+the host cores, on the sample named in its `sample` field.
+
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "prefill attn TFLOP/s (% MFMA peak) + decode tokens/s (% HBM BW), 1×MI355X"
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class EventPairs:
+    """K pairs of timing events whose raw hipEvent_t handles go to the
+    library, which records them on its launch stream around one kernel."""
+
+    def __init__(self, n: int):
+        import torch
+
+        self.pairs = []
+        for _ in range(n):
+            b = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            b.record()
+            e.record()
+            self.pairs.append((b, e))
+        torch.cuda.synchronize()
+
+    def handles(self, i: int) -> tuple[int, int]:
+        b, e = self.pairs[i]
+        return b.cuda_event, e.cuda_event
+
+    def mean_ms(self) -> float:
+        return statistics.fmean(b.elapsed_time(e) for b, e in self.pairs)
+
+
+def _time_steps(launch, steps: int, warmup: int):
+    """W untimed launches, then K timed ones bracketed by synchronisation;
+    returns (ms per step over the whole launch, ms per main kernel)."""
+    import torch
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    ev = EventPairs(steps)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        launch(timing=ev.handles(i))
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, ev.mean_ms()
+
+
+def _prefill_launch(w, inp, ops):
+    kw = {}
+    if "rope_cos" in inp:
+        kw.update(rope_cos=inp["rope_cos"], rope_sin=inp["rope_sin"], rope_q=True, rope_k=True)
+    if "alibi_slopes" in inp:
+        kw["alibi_slopes"] = inp["alibi_slopes"]
+    if w.lengths is not None:
+        kw.update(
+            cu_seqlens_q=inp["cu_seqlens"],
+            cu_seqlens_k=inp["cu_seqlens"],
+            max_seqlen_q=inp["max_seqlen"],
+            max_seqlen_k=inp["max_seqlen"],
+        )
+    return ops.plan_prefill(inp["q"], inp["k"], inp["v"], causal=w.causal, **kw)
+
+
+def _decode_launch(w, inp, ops):
+    kw = {}
+    if "rope_cos" in inp:
+        kw.update(rope_cos=inp["rope_cos"], rope_sin=inp["rope_sin"], rope_q=True)
+    return ops.plan_decode(
+        inp["q"], inp["k_cache"], inp["v_cache"], inp["cache_seqlens"], cache_layout=w.cache_layout, **kw
+    )
+
+
+def bench_prefill(w, steps, warmup):
+    from goda_amd import ops
+    from goda_amd import workloads as wl
+
+    inp = wl.prefill_inputs(w, "cuda")
+    launch = _prefill_launch(w, inp, ops)
+    ms, kms = _time_steps(launch, steps, warmup)
+    flops = wl.prefill_flops(w, inp.get("lengths"))
+    del launch, inp
+    return {
+        "workload": w.name,
+        "flops": flops,
+        "ms_per_step": ms,
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "kernel_ms": kms,
+        "kernel_tflops": flops / (kms * 1e-3) / 1e12,
+    }
+
+
+def bench_decode(w, steps, warmup):
+    from goda_amd import ops
+    from goda_amd import workloads as wl
+
+    inp = wl.decode_inputs(w, "cuda")
+    launch = _decode_launch(w, inp, ops)
+    ms, kms = _time_steps(launch, steps, warmup)
+    nbytes = wl.decode_bytes(w, inp["lengths"])
+    del launch, inp
+    return {
+        "workload": w.name,
+        "bytes": nbytes,
+        "ms_per_step": ms,
+        "tokens_per_s": w.batch / (ms * 1e-3),
+        "gbps": nbytes / (ms * 1e-3) / 1e9,
+        "kernel_ms": kms,
+        "kernel_gbps": nbytes / (kms * 1e-3) / 1e9,
+    }
+
+
+def _median_time(fn, reps: int) -> float:
+    fn()  # warm-up
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts)
+
+
+def cpu_baseline_prefill(w, reps: int = 3):
+    """The oracle's eager path (RoPE, then SDPA with goda's boolean causal
+    mask) in the workload dtype on the host cores, over the whole workload."""
+    import torch
+
+    from goda_amd import workloads as wl
+    from oracle import attention as ref
+
+    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    inp = wl.prefill_inputs(w, "cpu")
+    pos = torch.arange(w.seqlen)
+
+    def run():
+        q = ref.apply_rope(inp["q"], inp["rope_cos"], inp["rope_sin"], pos)
+        k = ref.apply_rope(inp["k"], inp["rope_cos"], inp["rope_sin"], pos)
+        return ref.attention(q, k, inp["v"], causal=True, dtype=w.dtype)
+
+    sec = _median_time(run, reps)
+    flops = wl.prefill_flops(w)
+    return {
+        "value": flops / sec / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"whole {w.name} (B={w.batch}, T={w.seqlen}) through oracle.attention in {str(w.dtype)[6:]}, "
+        f"median of {reps} after 1 warm-up: {sec:.3f} s",
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def cpu_baseline_decode(w, nseq: int = 8, reps: int = 3):
+    """The oracle's decode (per-sequence SDPA over the valid prefix) on the
+    first `nseq` sequences of the workload, scaled to tokens/s."""
+    import torch
+
+    from goda_amd import workloads as wl
+    from oracle import attention as ref
+
+    inp = wl.decode_inputs(w, "cuda")
+    lens = inp["lengths"][:nseq]
+    L = int(lens.max())
+    q = inp["q"][:nseq].cpu()
+    if w.cache_layout == "bhtd":
+        kc = inp["k_cache"][:nseq, :, :L].transpose(1, 2).cpu()
+        vc = inp["v_cache"][:nseq, :, :L].transpose(1, 2).cpu()
+    else:
+        kc = inp["k_cache"][:nseq, :L].cpu()
+        vc = inp["v_cache"][:nseq, :L].cpu()
+    del inp
+    torch.cuda.empty_cache()
+    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+
+    def run():
+        return ref.decode_attention_sdpa(q, kc, vc, lens, dtype=w.dtype)
+
+    sec = _median_time(run, reps)
+    return {
+        "value": nseq / sec,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"first {nseq} of {w.batch} sequences of {w.name} (keys {int(lens.sum())}), "
+        f"median of {reps}: {sec:.3f} s",
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(
+            "bench.py: this build measures one GPU only; the attention path has no multi-GPU "
+            "mode, so --gpus must be 1",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from goda_amd import workloads as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+
+    steps, warmup = args.steps, args.warmup
+    out: dict = {}
+    if args.only in (None, "prefill"):
+        _log("bench: cfg2 prefill")
+        p2 = bench_prefill(wl.CFG2, steps, warmup)
+        _log(f"  {p2}")
+        out["cfg2"] = p2
+    if args.only in (None, "decode"):
+        _log("bench: cfg4 decode")
+        d4 = bench_decode(wl.CFG4, steps, warmup)
+        _log(f"  {d4}")
+        out["cfg4"] = d4
+    if args.only is None:
+        _log("bench: cfg3 prefill")
+        out["cfg3"] = bench_prefill(wl.CFG3, steps, warmup)
+        _log(f"  {out['cfg3']}")
+        _log("bench: cfg5 mix")
+        p5 = bench_prefill(wl.CFG5.prefill, steps, warmup)
+        d5 = bench_decode(wl.CFG5.decode, steps, warmup)
+        out["cfg5"] = {"prefill": p5, "decode": d5}
+        _log(f"  {out['cfg5']}")
+
+    cpu = None
+    cpu_dec = None
+    if not args.no_cpu and args.only in (None, "prefill"):
+        _log("bench: CPU baseline (prefill)")
+        cpu = cpu_baseline_prefill(wl.CFG2)
+        _log(f"  {cpu}")
+    if not args.no_cpu and args.only in (None, "decode"):
+        _log("bench: CPU baseline (decode)")
+        cpu_dec = cpu_baseline_decode(wl.CFG4)
+        _log(f"  {cpu_dec}")
+
+    peak_tf = wl.BF16_PEAK_TFLOPS
+    peak_bw = wl.HBM_PEAK_GBPS
+    line: dict = {"metric": METRIC, "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True,
+                  "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded N(0,1)*0.5)"}
+    if "cfg2" in out:
+        p2 = out["cfg2"]
+        w = wl.CFG2
+        line.update(
+            value=round(p2["tflops"], 2),
+            unit="TFLOP/s",
+            ms_per_step=round(p2["ms_per_step"], 4),
+            dtype="bf16",
+            config={
+                "workload": w.name,
+                "batch": w.batch,
+                "seq_len": w.seqlen,
+                "heads_q": w.heads_q,
+                "heads_kv": w.heads_kv,
+                "head_dim": w.head_dim,
+                "causal": True,
+                "rope_base": w.rope_base,
+            },
+            mfma_peak_frac=round(p2["tflops"] / peak_tf, 4),
+            roofline={
+                "bound": "mfma",
+                "kernel": "prefill_mfma_kernel",
+                "achieved": round(p2["kernel_tflops"], 2),
+                "peak": peak_tf,
+                "unit": "TFLOP/s",
+                "frac": round(p2["kernel_tflops"] / peak_tf, 4),
+                "traffic": None,
+                "kernel_ms": round(p2["kernel_ms"], 4),
+                "flops_per_launch": p2["flops"],
+            },
+        )
+        if cpu is not None:
+            line["cpu_baseline"] = cpu
+    if "cfg4" in out:
+        d4 = out["cfg4"]
+        dec = {
+            "workload": wl.CFG4.name,
+            "value": round(d4["tokens_per_s"], 1),
+            "unit": "tokens/s",
+            "ms_per_step": round(d4["ms_per_step"], 4),
+            "hbm_frac": round(d4["gbps"] / peak_bw, 4),
+            "roofline": {
+                "bound": "hbm",
+                "kernel": "decode_splitk_kernel",
+                "achieved": round(d4["kernel_gbps"], 1),
+                "peak": peak_bw,
+                "unit": "GB/s",
+                "frac": round(d4["kernel_gbps"] / peak_bw, 4),
+                "traffic": None,
+                "kernel_ms": round(d4["kernel_ms"], 4),
+                "bytes_per_launch": d4["bytes"],
+            },
+        }
+        if cpu_dec is not None:
+            dec["cpu_baseline"] = cpu_dec
+        if "cfg2" in out:
+            line["decode"] = dec
+        else:
+            line.update(value=dec["value"], unit="tokens/s", ms_per_step=dec["ms_per_step"], dtype="bf16",
+                        config={"workload": wl.CFG4.name}, roofline=dec["roofline"])
+            if cpu_dec is not None:
+                line["cpu_baseline"] = cpu_dec
+    if "cfg3" in out:
+        c3 = out["cfg3"]
+        line["cfg3"] = {"tflops": round(c3["tflops"], 2), "mfma_peak_frac": round(c3["tflops"] / peak_tf, 4),
+                        "ms_per_step": round(c3["ms_per_step"], 4)}
+    if "cfg5" in out:
+        p5, d5 = out["cfg5"]["prefill"], out["cfg5"]["decode"]
+        line["cfg5"] = {
+            "prefill_tflops": round(p5["tflops"], 2),
+            "prefill_mfma_frac": round(p5["tflops"] / peak_tf, 4),
+            "prefill_ms": round(p5["ms_per_step"], 4),
+            "decode_tokens_per_s": round(d5["tokens_per_s"], 1),
+            "decode_hbm_frac": round(d5["gbps"] / peak_bw, 4),
+            "decode_ms": round(d5["ms_per_step"], 4),
+        }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

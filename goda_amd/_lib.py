@@ -80,6 +80,8 @@ class PrefillArgs(ctypes.Structure):
         ("reserved0", _i32),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
+        ("timing_begin", _vp),
+        ("timing_end", _vp),
     ]
 
 
@@ -121,6 +123,8 @@ class DecodeArgs(ctypes.Structure):
         ("reserved1", _i32),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
+        ("timing_begin", _vp),
+        ("timing_end", _vp),
     ]
 
 
@@ -189,6 +193,13 @@ def load() -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
+        # torch bundles its own HIP runtime with the same SONAME
+        # (libamdhip64.so.7); loading torch first makes the library bind to
+        # that one copy, so streams and events from torch are valid here.
+        try:
+            import torch  # noqa: F401
+        except ImportError:  # pragma: no cover - torch is a hard dependency
+            pass
         path = lib_path()
         if not path.exists():
             raise RuntimeError(

@@ -40,8 +40,9 @@ bool dtype_ok(int32_t d) { return d == GODA_DTYPE_F32 || d == GODA_DTYPE_F16 || 
 
 bool head_dim_ok(int32_t d) { return d == 64 || d == 128 || d == 256; }
 
-// Checks shared by prefill; returns GODA_OK or a failure status.
-int32_t check_prefill(const goda_prefill_args* a) {
+// Checks shared by prefill; returns GODA_OK or a failure status. The
+// workspace query passes need_ptrs = false: it depends on sizes only.
+int32_t check_prefill(const goda_prefill_args* a, bool need_ptrs) {
   if (!a) return fail(GODA_ERR_INVALID_ARG, "prefill: args is NULL");
   if (!dtype_ok(a->dtype)) return fail(GODA_ERR_INVALID_ARG, "prefill: unknown dtype %d", a->dtype);
   if (a->batch < 0 || a->seqlen_q < 0 || a->seqlen_k < 0)
@@ -57,8 +58,11 @@ int32_t check_prefill(const goda_prefill_args* a) {
     return fail(GODA_ERR_UNSUPPORTED, "prefill: head_dim %d not in {64, 128, 256}", a->head_dim);
   if ((a->cu_seqlens_q == nullptr) != (a->cu_seqlens_k == nullptr))
     return fail(GODA_ERR_INVALID_ARG, "prefill: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
+  if (!(a->softmax_scale > 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "prefill: softmax_scale must be positive (got %g)", (double)a->softmax_scale);
   if (a->batch == 0 || a->seqlen_q == 0) return GODA_OK;
-  if (!a->q || !a->k || !a->v || !a->o) return fail(GODA_ERR_INVALID_ARG, "prefill: NULL tensor pointer");
+  if (need_ptrs && (!a->q || !a->k || !a->v || !a->o))
+    return fail(GODA_ERR_INVALID_ARG, "prefill: NULL tensor pointer");
   if (a->rope_q || a->rope_k) {
     if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
       return fail(GODA_ERR_INVALID_ARG, "prefill: RoPE requested without cos/sin tables");
@@ -99,14 +103,14 @@ int64_t goda_attn_sizeof_kv_append_args(void) { return sizeof(goda_kv_append_arg
 const char* goda_attn_last_error(void) { return g_last_error.c_str(); }
 
 int64_t goda_attn_prefill_workspace_size(const goda_prefill_args* a) {
-  const int32_t st = check_prefill(a);
+  const int32_t st = check_prefill(a, false);
   if (st != GODA_OK) return st;
   if (goda::prefill_mfma_supported(*a)) return goda::prefill_mfma_workspace_bytes(*a);
   return 0;
 }
 
 int32_t goda_attn_prefill_fwd(const goda_prefill_args* a, void* stream) {
-  const int32_t st = check_prefill(a);
+  const int32_t st = check_prefill(a, true);
   if (st != GODA_OK) return st;
   if (a->batch == 0 || a->seqlen_q == 0) return ok();
   goda::PrefillParams p = make_prefill_params(a);
@@ -142,6 +146,8 @@ int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
   if (a->split_size < 0 || (a->split_size > 0 && a->split_size % 64 != 0))
     return fail(GODA_ERR_INVALID_ARG, "decode: split_size %d must be 0 or a positive multiple of 64",
                 a->split_size);
+  if (!(a->softmax_scale > 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "decode: softmax_scale must be positive (got %g)", (double)a->softmax_scale);
   if (a->batch == 0) return ok();
   if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->cache_seqlens)
     return fail(GODA_ERR_INVALID_ARG, "decode: NULL tensor pointer");
@@ -208,6 +214,8 @@ int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
   pa.rope_len = a->rope_len;
   pa.rope_q = a->rope_q;
   pa.rope_q_offset = a->rope_q_offset;
+  pa.timing_begin = a->timing_begin;
+  pa.timing_end = a->timing_end;
   goda::PrefillParams p = make_prefill_params(&pa);
   return hip_status(goda::launch_prefill_generic(p, s), "decode");
 }

@@ -108,8 +108,11 @@ __device__ __forceinline__ SeqGeom seq_geom(int b, int seqlen_q, int seqlen_k,
     g.k_row0 = 0;
     g.lk = seqlen_k;
   }
-  // Device-side lengths are clamped to the rows the tensors hold, so a bad
-  // value can shrink the work but never move a read out of bounds.
+  // Device-side lengths are clamped to the rows the launch was sized for
+  // (seqlen_q / seqlen_k, the maxima the host validated), so a bad value can
+  // shrink the work but never move a read out of bounds.
+  g.lq = max(0, min(g.lq, seqlen_q));
+  g.lk = max(0, min(g.lk, seqlen_k));
   if (seqused_k) g.lk = max(0, min(seqused_k[b], g.lk));
   return g;
 }

@@ -317,9 +317,12 @@ hipError_t launch_hd(const DecodeParams& p, hipStream_t s) {
   const goda_decode_args& a = p.a;
   const int nhs = (p.group + HMAX - 1) / HMAX;
   dim3 grid(p.nsplit_max, a.heads_kv * nhs, a.batch);
+  hipError_t e = record_timing(a.timing_begin, s);
+  if (e != hipSuccess) return e;
   decode_splitk_kernel<T, D, HMAX><<<grid, kWaves * 64, 0, s>>>(p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.nsplit_max <= 1) return e;
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = record_timing(a.timing_end, s)) != hipSuccess) return e;
+  if (p.nsplit_max <= 1) return hipSuccess;
   merge_kernel<T, D><<<dim3(a.heads_q, a.batch), D, 0, s>>>(p);
   return hipGetLastError();
 }

@@ -45,4 +45,10 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t s);
 
 hipError_t launch_kv_append(const goda_kv_append_args& a, hipStream_t s);
 
+// Records the caller's optional timing event (a hipEvent_t or NULL) on s.
+inline hipError_t record_timing(void* ev, hipStream_t s) {
+  if (!ev) return hipSuccess;
+  return hipEventRecord(reinterpret_cast<hipEvent_t>(ev), s);
+}
+
 }  // namespace goda

@@ -222,6 +222,8 @@ template <typename T>
 hipError_t launch_t(const PrefillParams& p, hipStream_t s) {
   const goda_prefill_args& a = p.a;
   dim3 grid((a.seqlen_q + kRows - 1) / kRows, a.heads_q, a.batch);
+  hipError_t e = record_timing(a.timing_begin, s);
+  if (e != hipSuccess) return e;
   switch (a.head_dim) {
     case 64:
       prefill_generic_kernel<T, 64><<<grid, kThreads, 0, s>>>(p);
@@ -235,7 +237,8 @@ hipError_t launch_t(const PrefillParams& p, hipStream_t s) {
     default:
       return hipErrorNotSupported;
   }
-  return hipGetLastError();
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return record_timing(a.timing_end, s);
 }
 
 }  // namespace

@@ -3,7 +3,7 @@
 //
 // Two launches per call:
 //   1. pack_kv_kernel: reads every K/V row of a KV head exactly once, applies
-//      RoPE to K (half-split rotation, mint/nn/pos.py:155-163), and writes
+//      RoPE to K (half-split rotation, mint/nn/pos.py:90-98), and writes
 //      tile-major copies to the workspace: K' tiles [BKV][D] and V^T tiles
 //      [D][BKV]. Rotating K here instead of inside the attention loop means
 //      each key is rotated once, not once per query tile and per query head.
@@ -443,8 +443,10 @@ hipError_t launch_attn(PrefillParams p, hipStream_t s) {
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
+  if ((e = record_timing(a.timing_begin, s)) != hipSuccess) return e;
   kern<<<dim3((unsigned)nblk), dim3(kWaves * 64), lds, s>>>(p);
-  return hipGetLastError();
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return record_timing(a.timing_end, s);
 }
 
 template <typename T, int D>

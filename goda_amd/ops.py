@@ -76,7 +76,41 @@ def _rope_tables(cos: torch.Tensor | None, sin: torch.Tensor | None, head_dim: i
     return cos, sin, cos.shape[0]
 
 
-def attention_prefill(
+class Launch:
+    """A validated, ready-to-run C-ABI call: the argument struct, the tensors
+    it points to (kept alive here), and the outputs. Calling it enqueues the
+    kernels on the current stream again; nothing is allocated or checked on
+    the Python side, so a serving loop can reuse one plan per shape.
+
+    `timing` optionally takes two hipEvent_t handles (e.g. the `cuda_event`
+    of two recorded torch.cuda.Event(enable_timing=True)) that the library
+    records right around its main kernel."""
+
+    def __init__(self, fn_name: str, args, keep: tuple, result):
+        self._fn = getattr(_lib.load(), fn_name)
+        self.args = args
+        self._keep = keep
+        self.result = result
+
+    def __call__(self, timing: tuple[int, int] | None = None):
+        a = self.args
+        if timing is not None:
+            a.timing_begin, a.timing_end = timing
+        try:
+            _lib.check(self._fn(ctypes.byref(a), _stream()))
+        finally:
+            if timing is not None:
+                a.timing_begin = a.timing_end = None
+        return self.result
+
+
+def attention_prefill(*args, **kwargs):
+    """Prefill attention through `goda_attn_prefill_fwd`; see `plan_prefill`
+    for the arguments. Returns `o` (and the fp32 `lse` if `return_lse`)."""
+    return plan_prefill(*args, **kwargs)()
+
+
+def plan_prefill(
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
@@ -99,12 +133,13 @@ def attention_prefill(
     return_lse: bool = False,
     out: torch.Tensor | None = None,
 ):
-    """Prefill attention through `goda_attn_prefill_fwd`.
+    """Validate the arguments of `goda_attn_prefill_fwd`, allocate outputs
+    and workspace, and return the `Launch` that runs it.
 
     Semantics are those of goda's eager path (mint/nn/flashattn.py:221-273):
     GQA head mapping h -> h // (Hq/Hkv), bottom-right causal alignment, left
     window only with causal (or a single query), ALiBi as
-    slope_h * (j - i_abs), RoPE as mint/nn/pos.py:155-177 using the given
+    slope_h * (j - i_abs), RoPE as mint/nn/pos.py:90-112 using the given
     fp32 cos/sin tables. Returns `o` (and `lse` fp32 if `return_lse`).
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
@@ -200,14 +235,20 @@ def attention_prefill(
     if need > 0:
         ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
-    # Temporaries (ws, slopes, tables) are freed after the launch is enqueued;
-    # the caching allocator only reuses them for work ordered after it on
-    # this stream.
-    _lib.check(lib.goda_attn_prefill_fwd(ctypes.byref(a), _stream()))
-    return (o, lse) if return_lse else o
+    # The plan keeps every tensor the struct points to alive. Once a plan is
+    # dropped, the caching allocator only reuses that memory for work
+    # ordered after the launch on this stream.
+    keep = (q, k, v, o, lse, ws, slopes, cos, sin, cu_q, cu_k, used)
+    return Launch("goda_attn_prefill_fwd", a, keep, (o, lse) if return_lse else o)
 
 
-def attention_decode(
+def attention_decode(*args, **kwargs):
+    """One-token decode through `goda_attn_decode`; see `plan_decode`.
+    Returns `o` (and the fp32 `lse` [B, Hq] if `return_lse`)."""
+    return plan_decode(*args, **kwargs)()
+
+
+def plan_decode(
     q: torch.Tensor,
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
@@ -225,7 +266,8 @@ def attention_decode(
     return_lse: bool = False,
     out: torch.Tensor | None = None,
 ):
-    """One-token decode over a KV cache with per-sequence lengths.
+    """Validate and prepare a one-token decode over a KV cache with
+    per-sequence lengths; returns the `Launch`.
 
     q: [B, Hq, D] (or [B, 1, Hq, D]); caches [B, Lmax, Hkv, D] when
     cache_layout == "bthd" (goda's KVCache, mint/kvcache/base.py:22-31) or
@@ -297,10 +339,9 @@ def attention_decode(
     if need > 0:
         ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
-    _lib.check(lib.goda_attn_decode(ctypes.byref(a), _stream()))
-    if squeeze:
-        o = o.unsqueeze(1)
-    return (o, lse) if return_lse else o
+    ov = o.unsqueeze(1) if squeeze else o
+    keep = (q, k_cache, v_cache, seqlens, o, lse, ws, slopes, cos, sin)
+    return Launch("goda_attn_decode", a, keep, (ov, lse) if return_lse else ov)
 
 
 def kv_append(

@@ -93,7 +93,7 @@ def _randn(shape, std, dtype, device, gen):
 
 def rope_tables(seq_len: int, head_dim: int, base: float, device="cpu", scale_factor: float = 1.0):
     """fp32 cos/sin [seq_len, head_dim/2] computed as goda's RoPE buffers
-    (mint/nn/pos.py:136-153; LinearScaledRoPE divides t, :192-213)."""
+    (mint/nn/pos.py:71-88; LinearScaledRoPE divides t, :127-148)."""
     channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
     inv_freq = 1.0 / (base ** (channel_range / head_dim))
     t = torch.arange(seq_len, dtype=torch.float32)
@@ -104,7 +104,7 @@ def rope_tables(seq_len: int, head_dim: int, base: float, device="cpu", scale_fa
 
 
 def alibi_slopes(n_heads: int) -> list[float]:
-    """goda's ALiBi slopes (mint/nn/pos.py:236-249)."""
+    """goda's ALiBi slopes (mint/nn/pos.py:171-184)."""
 
     def pow2(n: int) -> list[float]:
         start = 2 ** (-(2 ** -(math.log2(n) - 3)))

@@ -25,8 +25,8 @@
  *     queries and Lk keys sees key j iff j <= (Lk - Lq) + i;
  *   - left window W >= 0 additionally requires (Lk - Lq + i) - j <= W;
  *   - ALiBi adds slope[h] * (j - (Lk - Lq + i)) to the scaled score
- *     (mint/nn/pos.py:251-272);
- *   - RoPE is the half-split rotation of mint/nn/pos.py:155-163 with caller
+ *     (mint/nn/pos.py:186-207);
+ *   - RoPE is the half-split rotation of mint/nn/pos.py:90-98 with caller
  *     supplied fp32 cos/sin tables [rope_len, head_dim/2]; query row i is
  *     rotated at position rope_q_offset + (Lk - Lq) + i, key row j at
  *     rope_k_offset + j;
@@ -103,6 +103,12 @@ typedef struct goda_prefill_args {
 
   void* workspace;             /* size from goda_attn_prefill_workspace_size */
   int64_t workspace_bytes;
+
+  /* Optional hipEvent_t pair recorded on `stream` right before and right
+   * after the attention kernel itself (not the K/V pre-pass), so a caller
+   * can time that kernel alone. NULL: not recorded. */
+  void* timing_begin;
+  void* timing_end;
 } goda_prefill_args;
 
 typedef struct goda_decode_args {
@@ -139,6 +145,11 @@ typedef struct goda_decode_args {
 
   void* workspace;           /* size from goda_attn_decode_workspace_size */
   int64_t workspace_bytes;
+
+  /* Optional hipEvent_t pair recorded on `stream` right before and right
+   * after the split-K kernel (not the merge). NULL: not recorded. */
+  void* timing_begin;
+  void* timing_end;
 } goda_decode_args;
 
 typedef struct goda_kv_append_args {

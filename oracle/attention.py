@@ -21,9 +21,9 @@ import torch.nn.functional as F  # noqa: N812
 def rope_tables(seq_len: int, head_dim: int, base: float, scale_factor: float = 1.0):
     """cos/sin tables [seq_len, head_dim/2] in fp32.
 
-    mint/nn/pos.py:136-153 (RoPE._precompute_rotary_embeddings): inv_freq =
+    mint/nn/pos.py:71-88 (RoPE._precompute_rotary_embeddings): inv_freq =
     1 / base^(arange(0, D, 2)/D), freqs = outer(t, inv_freq). With
-    scale_factor != 1 it is LinearScaledRoPE (mint/nn/pos.py:192-213):
+    scale_factor != 1 it is LinearScaledRoPE (mint/nn/pos.py:127-148):
     t = arange(seq_len) / scale_factor.
     """
     channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
@@ -38,9 +38,9 @@ def rope_tables(seq_len: int, head_dim: int, base: float, scale_factor: float = 
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor):
     """Half-split rotation of x [..., T, H, D] at integer positions [T].
 
-    mint/nn/pos.py:155-163 (_apply_rotary_embs): x1 = x[..., :D/2],
+    mint/nn/pos.py:90-98 (_apply_rotary_embs): x1 = x[..., :D/2],
     x2 = x[..., D/2:], y = cat(x1 cos - x2 sin, x1 sin + x2 cos), with the
-    tables sliced at start_pos .. start_pos+T-1 (mint/nn/pos.py:165-177).
+    tables sliced at start_pos .. start_pos+T-1 (mint/nn/pos.py:100-112).
     Computed in the dtype of x (use fp32/fp64 inputs for the oracle).
     """
     c = cos[positions].to(x.dtype)[:, None, :]  # [T, 1, D/2]
@@ -51,7 +51,7 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions:
 
 
 def alibi_slopes(n_heads: int) -> list[float]:
-    """ALiBi slopes per head (mint/nn/pos.py:236-249).
+    """ALiBi slopes per head (mint/nn/pos.py:171-184).
 
     Power of two n: start = 2^(-2^-(log2 n - 3)) = 2^(-8/n), slope_h =
     start^(h+1). Otherwise the first 2^floor(log2 n) slopes, then every other
@@ -71,7 +71,7 @@ def alibi_slopes(n_heads: int) -> list[float]:
 def alibi_bias(slopes: torch.Tensor, q_len: int, k_len: int, dtype=torch.float32) -> torch.Tensor:
     """Additive bias [1, H, q_len, k_len]: slope_h * (j - i_abs).
 
-    mint/nn/pos.py:251-272 builds it for k_len = start_pos + q_len with query
+    mint/nn/pos.py:186-207 builds it for k_len = start_pos + q_len with query
     positions start_pos .. start_pos+q_len-1; here the query positions are
     bottom-right aligned, i_abs = (k_len - q_len) + i, which is the same thing.
     """
@@ -126,7 +126,7 @@ def sdpa_attention(
 
     q [B, Hq, Lq, D], k/v [B, Hkv, Lk, D]; enable_gqa when Hq != Hkv
     (mint/nn/flashattn.py:160). `alibi` [1|B, Hq, Lq, Lk] is the additive
-    bias the reference computes (mint/nn/pos.py:251-272) but never feeds to
+    bias the reference computes (mint/nn/pos.py:186-207) but never feeds to
     attention (mint/nn/attn.py:62); it is composed as SDPA's float mask with
     -inf where the boolean mask is False.
     """
@@ -326,6 +326,25 @@ def decode_attention(q, k_cache, v_cache, seqlens, *, window_left=-1, alibi_slop
         outs.append(o[0, 0])
         lses.append(lse[0, :, 0])
     return torch.stack(outs), torch.stack(lses)
+
+
+def decode_attention_sdpa(q, k_cache, v_cache, seqlens, *, window_left=-1, dtype=torch.float32):
+    """The reference's own decode call chain, restated: per sequence,
+    KVCache.update has made keys [0, L) valid (mint/kvcache/base.py:35-50),
+    then _attention_with_kvcache transposes to [B, H, L, D]
+    (mint/nn/flashattn.py:204-207) and calls _sdpa_attention with causal=True
+    and q_len = 1 (mint/nn/flashattn.py:209-218), which builds the
+    bottom-right boolean mask and runs SDPA with enable_gqa.
+    q [B, Hq, D], caches [B, >=L, Hkv, D] -> o [B, Hq, D] in `dtype`."""
+    outs = []
+    for b in range(q.shape[0]):
+        L = int(seqlens[b])
+        qs = q[b].to("cpu", dtype)[None, :, None, :]  # [1, Hq, 1, D]
+        ks = k_cache[b, :L].to("cpu", dtype).transpose(0, 1)[None]  # [1, Hkv, L, D]
+        vs = v_cache[b, :L].to("cpu", dtype).transpose(0, 1)[None]
+        o = sdpa_attention(qs, ks, vs, causal=True, window_size=(window_left, -1))
+        outs.append(o[0, :, 0])
+    return torch.stack(outs)
 
 
 def merge_splits(o_parts: torch.Tensor, lse_parts: torch.Tensor):

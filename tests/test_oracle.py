@@ -1,0 +1,300 @@
+"""Pins the CPU oracle (oracle/attention.py) before it is trusted as the
+checker of the HIP kernels. The reference ships no golden vectors for this
+path, so each function is pinned by an independent float64 brute force
+(oracle/brute.py, explicit loops), closed forms, or invariants — chosen so
+that a dropped term, a wrong sign or index, or a transposed operand fails.
+The `test_planted_*` cases plant such mistakes in a copy of the oracle's
+inputs/formulas and assert that the checks catch them."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ref
+from oracle import brute
+
+F64 = torch.float64
+
+
+def _rand(shape, seed, dtype=F64):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float64).to(dtype)
+
+
+def _brute(q, k, v, **kw):
+    o, lse = brute.attention(q.numpy(), k.numpy(), v.numpy(), **kw)
+    return torch.from_numpy(o), torch.from_numpy(lse)
+
+
+# ---------------------------------------------------------------------------
+# attention core: SDPA restatement vs explicit-loop brute force
+# ---------------------------------------------------------------------------
+CASES = [
+    # b, tq, tk, hq, hkv, d, causal
+    (1, 5, 5, 2, 2, 8, True),
+    (2, 7, 7, 4, 2, 8, True),
+    (2, 3, 9, 6, 2, 16, True),  # Lq < Lk: bottom-right alignment
+    (1, 6, 6, 4, 1, 8, False),  # MQA
+    (2, 4, 11, 8, 4, 8, False),
+]
+
+
+@pytest.mark.parametrize("b,tq,tk,hq,hkv,d,causal", CASES)
+def test_sdpa_matches_brute(b, tq, tk, hq, hkv, d, causal):
+    q, k, v = _rand((b, tq, hq, d), 1), _rand((b, tk, hkv, d), 2), _rand((b, tk, hkv, d), 3)
+    o = ref.attention(q, k, v, causal=causal, dtype=F64)
+    o_b, lse_b = _brute(q, k, v, causal=causal)
+    assert torch.allclose(o, o_b, atol=1e-12)
+    o_r, lse_r = ref.attention_rows(q, k, v, torch.arange(tq), causal=causal, dtype=F64)
+    assert torch.allclose(o_r, o_b, atol=1e-12)
+    assert torch.allclose(lse_r, lse_b, atol=1e-12)
+
+
+@pytest.mark.parametrize("window", [0, 1, 3, 20])
+def test_window_matches_brute(window):
+    b, tq, tk, hq, hkv, d = 2, 6, 10, 4, 2, 8
+    q, k, v = _rand((b, tq, hq, d), 4), _rand((b, tk, hkv, d), 5), _rand((b, tk, hkv, d), 6)
+    o = ref.attention(q, k, v, causal=True, window_size=(window, -1), dtype=F64)
+    o_b, lse_b = _brute(q, k, v, causal=True, window_left=window)
+    assert torch.allclose(o, o_b, atol=1e-12)
+    o_r, lse_r = ref.attention_rows(q, k, v, torch.arange(tq), causal=True, window_left=window, dtype=F64)
+    assert torch.allclose(o_r, o_b, atol=1e-12) and torch.allclose(lse_r, lse_b, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_alibi_matches_brute(causal):
+    b, tq, tk, hq, hkv, d = 1, 5, 8, 4, 1, 8
+    q, k, v = _rand((b, tq, hq, d), 7), _rand((b, tk, hkv, d), 8), _rand((b, tk, hkv, d), 9)
+    slopes = torch.tensor(ref.alibi_slopes(hq), dtype=F64)
+    o = ref.attention(q, k, v, causal=causal, alibi_slopes=slopes, dtype=F64)
+    o_b, lse_b = _brute(q, k, v, causal=causal, slopes=slopes.numpy())
+    assert torch.allclose(o, o_b, atol=1e-12)
+    o_r, lse_r = ref.attention_rows(q, k, v, torch.arange(tq), causal=causal, alibi_slopes=slopes, dtype=F64)
+    assert torch.allclose(o_r, o_b, atol=1e-12) and torch.allclose(lse_r, lse_b, atol=1e-12)
+
+
+def test_scale_matches_brute():
+    q, k, v = _rand((1, 4, 2, 8), 10), _rand((1, 4, 2, 8), 11), _rand((1, 4, 2, 8), 12)
+    o = ref.attention(q, k, v, causal=True, scale=0.37, dtype=F64)
+    o_b, _ = _brute(q, k, v, causal=True, scale=0.37)
+    assert torch.allclose(o, o_b, atol=1e-12)
+
+
+def test_doc_ids_match_brute_and_varlen():
+    b, t, hq, hkv, d = 2, 9, 4, 2, 8
+    q, k, v = _rand((b, t, hq, d), 13), _rand((b, t, hkv, d), 14), _rand((b, t, hkv, d), 15)
+    doc = torch.tensor([[0, 0, 0, 1, 1, 2, 2, 2, 2], [5, 5, 5, 5, 5, 6, 6, 7, 7]])
+    o = ref.attention(q, k, v, causal=True, doc_ids=doc, dtype=F64)
+    o_b, _ = _brute(q, k, v, causal=True, doc_ids=doc.numpy())
+    assert torch.allclose(o, o_b, atol=1e-12)
+    cu = ref.doc_ids_to_cu_seqlens(doc)
+    assert cu.tolist() == [0, 3, 5, 9, 14, 16, 18]
+    o_v = ref.varlen_attention(q.reshape(-1, hq, d), k.reshape(-1, hkv, d), v.reshape(-1, hkv, d), cu, cu,
+                               causal=True, dtype=F64)
+    assert torch.allclose(o_v.reshape(b, t, hq, d), o_b, atol=1e-12)
+
+
+def test_causal_square_equals_is_causal():
+    """With Lq == Lk and no other mask, goda's explicit boolean mask equals
+    SDPA's is_causal=True (mint/nn/flashattn.py:245-273)."""
+    q, k, v = _rand((1, 3, 7, 8), 16), _rand((1, 3, 7, 8), 17), _rand((1, 3, 7, 8), 18)
+    o_mask = ref.sdpa_attention(q, k, v, causal=True)
+    o_is = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+    assert torch.allclose(o_mask, o_is, atol=1e-12)
+
+
+def test_gqa_equals_repeated_mha():
+    b, t, hq, hkv, d = 2, 6, 6, 2, 8
+    q, k, v = _rand((b, t, hq, d), 19), _rand((b, t, hkv, d), 20), _rand((b, t, hkv, d), 21)
+    o = ref.attention(q, k, v, causal=True, dtype=F64)
+    rep = hq // hkv
+    o_mha = ref.attention(q, k.repeat_interleave(rep, 2), v.repeat_interleave(rep, 2), causal=True, dtype=F64)
+    assert torch.allclose(o, o_mha, atol=1e-12)
+
+
+def test_brute_lse_closed_form():
+    """One key: o = v, lse = the single scaled score."""
+    q, k, v = _rand((1, 1, 1, 4), 22), _rand((1, 1, 1, 4), 23), _rand((1, 1, 1, 4), 24)
+    o, lse = _brute(q, k, v, causal=True)
+    s = float((q[0, 0, 0] * k[0, 0, 0]).sum()) / 2.0
+    assert torch.allclose(o, v) and abs(float(lse[0, 0, 0]) - s) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+def test_rope_tables_closed_form():
+    cos, sin = ref.rope_tables(64, 16, 10000.0)
+    p, i = 37, 5
+    theta = p * 10000.0 ** (-(2.0 * i) / 16)
+    assert abs(float(cos[p, i]) - math.cos(theta)) < 1e-5
+    assert abs(float(sin[p, i]) - math.sin(theta)) < 1e-5
+    cos_s, _ = ref.rope_tables(64, 16, 10000.0, scale_factor=4.0)
+    assert abs(float(cos_s[p, i]) - math.cos(theta / 4.0)) < 1e-5
+
+
+def test_rope_matches_brute_and_invariants():
+    t, h, d = 24, 3, 16
+    x = _rand((2, t, h, d), 25)
+    cos, sin = ref.rope_tables(t, d, 10000.0)
+    pos = torch.arange(t)
+    y = ref.apply_rope(x, cos.to(F64), sin.to(F64), pos)
+    y_b = torch.from_numpy(brute.rope(x.numpy(), pos.numpy(), 10000.0))
+    assert torch.allclose(y, y_b, atol=1e-5)
+    # position 0 is the identity
+    assert torch.allclose(y[:, 0], x[:, 0])
+    # each (i, i + D/2) pair keeps its norm
+    n_x = x[..., : d // 2] ** 2 + x[..., d // 2 :] ** 2
+    n_y = y[..., : d // 2] ** 2 + y[..., d // 2 :] ** 2
+    assert torch.allclose(n_x, n_y, atol=1e-10)
+
+
+def test_rope_relative_positions():
+    """q_m . k_n depends only on m - n (float64 tables from the closed form)."""
+    d = 16
+    q, k = _rand((1, 1, 1, d), 26), _rand((1, 1, 1, d), 27)
+    half = torch.arange(0, d, 2, dtype=F64)
+    inv = 1.0 / (10000.0 ** (half / d))
+    ang = torch.outer(torch.arange(40, dtype=F64), inv)
+    cos, sin = ang.cos(), ang.sin()
+
+    def dot(m, n):
+        qm = ref.apply_rope(q, cos, sin, torch.tensor([m]))
+        kn = ref.apply_rope(k, cos, sin, torch.tensor([n]))
+        return float((qm * kn).sum())
+
+    assert abs(dot(10, 3) - dot(30, 23)) < 1e-10
+    assert abs(dot(5, 5) - dot(0, 0)) < 1e-10
+    assert abs(dot(10, 3) - dot(3, 10)) > 1e-6  # not symmetric in general
+
+
+# ---------------------------------------------------------------------------
+# ALiBi
+# ---------------------------------------------------------------------------
+def test_alibi_slopes_closed_form():
+    # n = 16 (cfg3): s_h = 2^(-(h+1)/2) for 0-based h
+    assert np.allclose(ref.alibi_slopes(16), [2.0 ** (-(h + 1) / 2) for h in range(16)], rtol=1e-14)
+    # n = 8: 2^-1 ... 2^-8
+    assert np.allclose(ref.alibi_slopes(8), [2.0 ** (-(h + 1)) for h in range(8)], rtol=1e-14)
+    # non power of two: the 4 slopes of n=4, then every other slope of n=8
+    assert np.allclose(ref.alibi_slopes(6), [2**-2, 2**-4, 2**-6, 2**-8, 2**-1, 2**-3], rtol=1e-14)
+
+
+def test_alibi_bias_sign_and_diagonal():
+    slopes = torch.tensor([0.5, 0.25], dtype=F64)
+    bias = ref.alibi_bias(slopes, 3, 5, F64)  # queries at absolute 2, 3, 4
+    assert bias.shape == (1, 2, 3, 5)
+    assert float(bias[0, 0, 0, 2]) == 0.0 and float(bias[0, 1, 2, 4]) == 0.0
+    assert float(bias[0, 0, 0, 0]) == -1.0  # key 2 positions back: 0.5 * -2
+    assert float(bias[0, 1, 2, 1]) == -0.75
+
+
+# ---------------------------------------------------------------------------
+# decode, KV cache and split-K merge
+# ---------------------------------------------------------------------------
+def test_decode_equals_last_prefill_row_and_reference_chain():
+    b, lmax, hq, hkv, d = 3, 20, 4, 2, 8
+    lens = torch.tensor([1, 9, 20], dtype=torch.int32)
+    q, kc, vc = _rand((b, hq, d), 28), _rand((b, lmax, hkv, d), 29), _rand((b, lmax, hkv, d), 30)
+    o, lse = ref.decode_attention(q, kc, vc, lens, dtype=F64)
+    o_sdpa = ref.decode_attention_sdpa(q, kc, vc, lens, dtype=F64)
+    assert torch.allclose(o, o_sdpa, atol=1e-12)
+    for i in range(b):
+        L = int(lens[i])
+        o_b, lse_b = _brute(q[i][None, None], kc[i : i + 1, :L], vc[i : i + 1, :L], causal=True)
+        assert torch.allclose(o[i], o_b[0, 0], atol=1e-12)
+        assert torch.allclose(lse[i], lse_b[0, :, 0], atol=1e-12)
+
+
+def test_decode_window_matches_brute():
+    b, lmax, hq, hkv, d, w = 2, 16, 2, 1, 8, 4
+    lens = torch.tensor([3, 16], dtype=torch.int32)
+    q, kc, vc = _rand((b, hq, d), 31), _rand((b, lmax, hkv, d), 32), _rand((b, lmax, hkv, d), 33)
+    o, _ = ref.decode_attention(q, kc, vc, lens, window_left=w, dtype=F64)
+    o2 = ref.decode_attention_sdpa(q, kc, vc, lens, window_left=w, dtype=F64)
+    for i in range(b):
+        L = int(lens[i])
+        o_b, _ = _brute(q[i][None, None], kc[i : i + 1, :L], vc[i : i + 1, :L], causal=True, window_left=w)
+        assert torch.allclose(o[i], o_b[0, 0], atol=1e-12) and torch.allclose(o2[i], o_b[0, 0], atol=1e-12)
+
+
+@pytest.mark.parametrize("splits", [[], [1], [3, 7], [1, 2, 3, 4, 5, 6, 7, 8, 9]])
+def test_split_merge_independent_of_splits(splits):
+    L, h, d = 10, 3, 8
+    q, k, v = _rand((h, d), 34), _rand((L, h, d), 35), _rand((L, h, d), 36)
+    o, lse = ref.split_attention(q, k, v, splits)
+    o_b, lse_b = _brute(q[None, None], k[None], v[None], causal=False)
+    assert torch.allclose(o, o_b[0, 0], atol=1e-12)
+    assert torch.allclose(lse, lse_b[0, :, 0], atol=1e-12)
+
+
+def test_merge_handles_empty_split():
+    o_parts = torch.stack([torch.ones(2, 4), torch.zeros(2, 4)]).to(F64)
+    lse_parts = torch.tensor([[0.0, 1.0], [-math.inf, -math.inf]], dtype=F64)
+    o, lse = ref.merge_splits(o_parts, lse_parts)
+    assert torch.allclose(o, torch.ones(2, 4, dtype=F64)) and torch.allclose(lse, lse_parts[0])
+
+
+def test_kvcache_oracle_matches_reference_update():
+    """Equal lengths: append == KVCache.update at start_pos = seqlens[0]
+    (mint/kvcache/base.py:35-50), restated with plain slicing."""
+    b, lmax, h, d = 2, 10, 2, 4
+    c = ref.KVCacheOracle(b, lmax, h, d, dtype=F64)
+    k_ref = torch.zeros(b, lmax, h, d, dtype=F64)
+    pos = 0
+    for step, tn in enumerate([3, 1, 2]):
+        kn = _rand((b, tn, h, d), 40 + step)
+        c.append(kn, kn)
+        k_ref[:b, pos : pos + tn] = kn
+        pos += tn
+        assert c.seqlens.tolist() == [pos] * b
+    assert torch.equal(c.k, k_ref) and torch.equal(c.v, k_ref)
+
+
+# ---------------------------------------------------------------------------
+# planted mistakes: the checks above must catch each of them
+# ---------------------------------------------------------------------------
+def test_planted_wrong_gqa_mapping_is_caught():
+    b, t, hq, hkv, d = 1, 5, 4, 2, 8
+    q, k, v = _rand((b, t, hq, d), 50), _rand((b, t, hkv, d), 51), _rand((b, t, hkv, d), 52)
+    o_b, _ = _brute(q, k, v, causal=True)
+    # h % Hkv instead of h // (Hq/Hkv)
+    idx = torch.tensor([h % hkv for h in range(hq)])
+    o_bad = ref.attention(q, k[:, :, idx], v[:, :, idx], causal=True, dtype=F64)
+    assert not torch.allclose(o_bad, o_b, atol=1e-6)
+
+
+def test_planted_top_left_causal_is_caught():
+    b, tq, tk, h, d = 1, 3, 8, 2, 8
+    q, k, v = _rand((b, tq, h, d), 53), _rand((b, tk, h, d), 54), _rand((b, tk, h, d), 55)
+    o_b, _ = _brute(q, k, v, causal=True)
+    o_bad = torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True
+    ).transpose(1, 2)  # top-left aligned for Lq < Lk
+    assert not torch.allclose(o_bad, o_b, atol=1e-6)
+
+
+def test_planted_alibi_sign_is_caught():
+    b, t, h, d = 1, 6, 2, 8
+    q, k, v = _rand((b, t, h, d), 56), _rand((b, t, h, d), 57), _rand((b, t, h, d), 58)
+    slopes = torch.tensor(ref.alibi_slopes(h), dtype=F64)
+    o_b, _ = _brute(q, k, v, causal=True, slopes=slopes.numpy())
+    o_bad = ref.attention(q, k, v, causal=True, alibi_slopes=-slopes, dtype=F64)
+    assert not torch.allclose(o_bad, o_b, atol=1e-6)
+
+
+def test_planted_rope_pairing_is_caught():
+    """Interleaved (2i, 2i+1) pairing instead of goda's half-split pairing."""
+    t, d = 6, 8
+    x = _rand((1, t, 1, d), 59)
+    pos = torch.arange(t)
+    y_b = torch.from_numpy(brute.rope(x.numpy(), pos.numpy(), 10000.0))
+    cos, sin = ref.rope_tables(t, d, 10000.0)
+    xi = x.reshape(1, t, 1, d // 2, 2)
+    c, s = cos.to(F64)[:, None, :], sin.to(F64)[:, None, :]
+    y_bad = torch.stack([xi[..., 0] * c - xi[..., 1] * s, xi[..., 0] * s + xi[..., 1] * c], -1).reshape(1, t, 1, d)
+    assert not torch.allclose(y_bad, y_b, atol=1e-4)
