@@ -2,29 +2,41 @@
 // (bf16 or fp16 operands, fp32 accumulation).
 //
 // Two launches per call:
-//   1. pack_kv_kernel: reads every K/V row of a KV head exactly once, applies
-//      RoPE to K (half-split rotation, mint/nn/pos.py:90-98), and writes
-//      tile-major copies to the workspace: K' tiles [BKV][D] and V^T tiles
-//      [D][BKV]. Rotating K here instead of inside the attention loop means
-//      each key is rotated once, not once per query tile and per query head.
-//   2. prefill_mfma_kernel: one workgroup per (query tile, query-head slice,
-//      sequence). All waves of a workgroup belong to query heads of ONE KV
-//      head, so every K/V tile brought into LDS serves HG query heads ("read
-//      once per query-head group"). Per wave: 32*NT query rows of one head.
+//   1. pack_kv_kernel reads every K/V row of a KV head once, rotates K (RoPE,
+//      half-split pairing of mint/nn/pos.py:90-98) and writes, per tile of BKV
+//      keys, the exact byte image the attention kernel wants in LDS:
+//        K' image   [D/8 chunks][BKV keys]    of 16-byte chunks (8 elements)
+//        V^T image  [BKV/8 chunks][D dims]    of 16-byte chunks
+//      "Chunk-column-major": the 16 lanes of a quarter-wave that read one
+//      MFMA operand column touch 256 consecutive bytes, so LDS reads are
+//      conflict-free without padding or XOR swizzles, and every operand
+//      address is one per-lane base plus a compile-time offset.
+//      Inside each 16-key group of the V^T image the keys are stored in the
+//      order the P^T register fragment holds them (kPermKey), so one 16-byte
+//      read yields a whole MFMA operand.
+//   2. prefill_fa_kernel: one workgroup (4 waves, one per SIMD) per (query
+//      tile, query-head slice, sequence). All waves belong to query heads of
+//      ONE KV head, so every K/V tile streamed into LDS serves the whole
+//      query-head group ("read once per group"). Tiles arrive by direct
+//      global->LDS DMA (global_load_lds_dwordx4) into a ring of STAGES
+//      buffers, STAGES-1 tiles ahead of use.
 //
-// GEMM shapes per wave and KV tile (32x32x16 MFMA):
-//   S^T[kv][q] = K'[kv][d] . Q^T[d][q]     A = K' from LDS, B = Q^T in VGPRs
-//   O^T[d][q] += V^T[d][kv] . P^T[kv][q]   A = V^T from LDS, B = P^T in VGPRs
-// Computing the transposed products keeps every query row in one lane pair
-// (lanes l and l^32), so the online softmax needs a single cross-lane max per
-// tile and the output rescale is lane-local.
+// Per wave and KV tile (32x32x16 MFMA, 32*NT query rows of one head):
+//   S^T[kv][q] = K'[kv][d] . Q^T[d][q]     A = K' (LDS), B = Q^T (registers)
+//   O^T[d][q] += V^T[d][kv] . P^T[kv][q]   A = V^T (LDS), B = P^T (registers)
+// Every query row lives in one lane pair (l, l^32), so the row max needs one
+// permlane32 swap and any rescale is lane-local. The loop is software
+// pipelined: the MFMAs of S(j+1) are issued next to the exp / convert /
+// row-sum VALU work on S(j); P(j)V(j) follows.
+// Rescaling is lazy: a row's reference max only moves (and its O and l are
+// rescaled) when the tile max exceeds it by more than kRescaleThresh (log2
+// units), so O is untouched by the VALU on almost every tile. The result is
+// exact either way: numerator and denominator share the reference max.
 //
 // MFMA 32x32 accumulator layout (gfx9 family): lane l, register r holds
-// row 8*(r/4) + 4*(l/32) + r%4, column l%32. The layout of the K dimension
-// inside the A/B operands is the same function for A and B, so any
-// consistent assignment of k indices to (lane half, element) is valid; the
-// P^T operand reuses the S^T accumulator layout and V^T is read with that
-// same assignment.
+// row 8*(r/4) + 4*(l/32) + r%4, column l%32. The K dimension of the A and B
+// operands uses the same (lane half, element) assignment, so the P^T operand
+// is the S^T accumulator re-packed in place.
 
 #include "common.h"
 #include "launch.h"
@@ -32,7 +44,7 @@
 namespace goda {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr float kRescaleThresh = 8.0f;  // log2 units: P entries stay <= 2^8
 
 template <typename T>
 struct Vec;
@@ -47,26 +59,52 @@ struct Vec<f16> {
   typedef f16x4 v4;
 };
 
-template <int D, int BKV>
-struct Tile {
-  static constexpr int KLD = D + 8;    // K' LDS row stride (elements), 16-B aligned rows
-  static constexpr int VLD = BKV + 4;  // V^T LDS row stride: rows shift by 2 banks
-  static constexpr int K_ELEMS = BKV * KLD;
-  static constexpr int V_ELEMS = D * VLD;
-  static constexpr int STAGE_ELEMS = K_ELEMS + V_ELEMS;
+// Position p (0..15) inside a 16-key group of the V^T image holds key
+// kPermKey(p) of that group: the P^T fragment of lane half h carries keys
+// {4h..4h+3, 8+4h..8+4h+3} of each group (accumulator rows of S^T).
+__host__ __device__ constexpr int kPermKey(int p) { return 8 * ((p % 8) / 4) + 4 * (p / 8) + p % 4; }
+
+template <int D, int BKV, int WAVES>
+struct TileGeom {
+  static constexpr int K_CHUNKS = D / 8 * BKV;  // 16-byte chunks of the K' image
+  static constexpr int V_CHUNKS = BKV / 8 * D;
+  static constexpr int BYTES = (K_CHUNKS + V_CHUNKS) * 16;
+  static constexpr int DMA_PER_WAVE = (K_CHUNKS + V_CHUNKS) / (64 * WAVES);
+  static_assert((K_CHUNKS + V_CHUNKS) % (64 * WAVES) == 0, "tile must split evenly over the waves");
 };
 
-// Shared by both launches: index of workspace tile j of sequence b, KV head hk.
+// Index of workspace tile j of sequence b, KV head hk.
 __device__ __forceinline__ int64_t ws_tile(int b, int j, int hk, int ntiles, int hkv) {
   return ((int64_t)b * ntiles + j) * hkv + hk;
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Wait until at most `groups` DMA groups of PER instructions are in flight.
+template <int PER, int MAXG>
+__device__ __forceinline__ void wait_dma_groups(int groups) {
+  if constexpr (MAXG > 0) {
+    if (groups >= MAXG) {
+      wait_vmcnt<MAXG * PER>();
+      return;
+    }
+    wait_dma_groups<PER, MAXG - 1>(groups);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 // ---------------------------------------------------------------------------
-// 1. pack K (rotated) and V^T into tile-major workspace
+// 1. pack K (rotated) and V^T into tile images
 // ---------------------------------------------------------------------------
 template <typename T, int D, int BKV>
 __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
   typedef typename Vec<T>::v8 v8;
+  typedef TileGeom<D, BKV, 1> TG;
   const goda_prefill_args& a = p.a;
   const int j = blockIdx.x;
   const int hk = blockIdx.y;
@@ -76,93 +114,134 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
   const int kv0 = j * BKV;
   if (kv0 >= g.lk) return;
 
-  T* kp = reinterpret_cast<T*>(a.workspace);
-  const int64_t tile_elems = (int64_t)BKV * D;
-  const int64_t ntot = (int64_t)a.batch * p.ntiles_k * a.heads_kv;
-  T* vt = kp + ntot * tile_elems;
-  const int64_t t = ws_tile(b, j, hk, p.ntiles_k, a.heads_kv);
-  T* kdst = kp + t * tile_elems;
-  T* vdst = vt + t * tile_elems;
+  unsigned char* tile = reinterpret_cast<unsigned char*>(a.workspace) +
+                        ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES;
+  v8* kimg = reinterpret_cast<v8*>(tile);
+  v8* vimg = reinterpret_cast<v8*>(tile + TG::K_CHUNKS * 16);
 
   const T* kbase = reinterpret_cast<const T*>(a.k) +
                    (a.cu_seqlens_k ? 0 : (int64_t)b * a.k_stride_b) + (int64_t)hk * a.k_stride_h;
   const T* vbase = reinterpret_cast<const T*>(a.v) +
                    (a.cu_seqlens_k ? 0 : (int64_t)b * a.v_stride_b) + (int64_t)hk * a.v_stride_h;
 
-  // V rows staged for the transpose; +8 elements keep columns off one bank.
-  __shared__ T vs[BKV][D + 8];
-
+  // One row-major staging buffer, used for K then for V; +8 elements per row
+  // keep the column reads of the transposes off a single bank.
+  __shared__ __align__(16) T rows[BKV][D + 8];
   const int tid = threadIdx.x;
   constexpr int HALF8 = D / 16;  // 8-element chunks per half row
+
+  // K: coalesced row loads, rotation of the (i, i + D/2) pairs, staged.
   for (int idx = tid; idx < BKV * HALF8; idx += 256) {
     const int r = idx / HALF8;
     const int c = (idx % HALF8) * 8;
     const int row = kv0 + r;
-    v8 k1 = {}, k2 = {}, v1 = {}, v2 = {};
+    v8 k1 = {}, k2 = {};
     if (row < g.lk) {
-      const int64_t roff = (g.k_row0 + row);
-      const T* kr = kbase + roff * a.k_stride_t;
-      const T* vr = vbase + roff * a.v_stride_t;
+      const T* kr = kbase + (g.k_row0 + row) * a.k_stride_t;
       k1 = ld_vec<v8>(kr + c);
       k2 = ld_vec<v8>(kr + c + D / 2);
-      v1 = ld_vec<v8>(vr + c);
-      v2 = ld_vec<v8>(vr + c + D / 2);
       if (a.rope_k) {
         const int pos = a.rope_k_offset + row;
         const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
         const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
+        const f32x4 c0 = ld_vec<f32x4>(cs), c1 = ld_vec<f32x4>(cs + 4);
+        const f32x4 s0 = ld_vec<f32x4>(sn), s1 = ld_vec<f32x4>(sn + 4);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float x1 = (float)k1[e], x2 = (float)k2[e];
-          const float cc = cs[e], ss = sn[e];
+          const float cc = e < 4 ? c0[e & 3] : c1[e & 3];
+          const float ss = e < 4 ? s0[e & 3] : s1[e & 3];
           k1[e] = (T)(x1 * cc - x2 * ss);
           k2[e] = (T)(x1 * ss + x2 * cc);
         }
       }
     }
-    st_vec<v8>(kdst + r * D + c, k1);
-    st_vec<v8>(kdst + r * D + c + D / 2, k2);
-    st_vec<v8>(&vs[r][c], v1);
-    st_vec<v8>(&vs[r][c + D / 2], v2);
+    st_vec<v8>(&rows[r][c], k1);
+    st_vec<v8>(&rows[r][c + D / 2], k2);
   }
   __syncthreads();
-  // V^T: thread writes 8 consecutive keys of one head-dim row.
-  constexpr int RCH = BKV / 8;
-  for (int idx = tid; idx < D * RCH; idx += 256) {
-    const int d = idx / RCH;
-    const int r0 = (idx % RCH) * 8;
+  // K' image: chunk (c, r) at c*BKV + r; consecutive threads write
+  // consecutive chunks.
+  for (int idx = tid; idx < TG::K_CHUNKS; idx += 256) {
+    const int c = idx / BKV, r = idx % BKV;
+    kimg[idx] = ld_vec<v8>(&rows[r][8 * c]);
+  }
+  __syncthreads();
+  // V rows; rows past the sequence end are zero, so P = 0 there meets a
+  // finite value.
+  for (int idx = tid; idx < BKV * (D / 8); idx += 256) {
+    const int r = idx / (D / 8);
+    const int c = (idx % (D / 8)) * 8;
+    const int row = kv0 + r;
+    v8 v = {};
+    if (row < g.lk) v = ld_vec<v8>(vbase + (g.k_row0 + row) * a.v_stride_t + c);
+    st_vec<v8>(&rows[r][c], v);
+  }
+  __syncthreads();
+  // V^T image: chunk (kc, d) at kc*D + d holds keys kPermKey(8*(kc%2) + e),
+  // e = 0..7, of the 16-key group kc/2.
+  for (int idx = tid; idx < TG::V_CHUNKS; idx += 256) {
+    const int kc = idx / D, d = idx % D;
+    const int k0 = 16 * (kc / 2);
     v8 out;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = vs[r0 + e][d];
-    st_vec<v8>(vdst + (int64_t)d * BKV + r0, out);
+    for (int e = 0; e < 8; ++e) out[e] = rows[k0 + kPermKey(8 * (kc % 2) + e)][d];
+    vimg[idx] = out;
   }
 }
 
 // ---------------------------------------------------------------------------
 // 2. attention
 // ---------------------------------------------------------------------------
-template <typename T, int D, int BKV, int NT, bool ALIBI>
-__global__ void __launch_bounds__(kWaves * 64, 1) prefill_mfma_kernel(const PrefillParams p) {
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+// After permlane32_swap(x, x), r[0] holds x of lane l%32 and r[1] x of lane
+// 32 + l%32: the two halves of a query row.
+__device__ __forceinline__ float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// acc + p[2i] + p[2i+1] on the rounded probabilities (the values the PV
+// product uses).
+__device__ __forceinline__ float dot2_ones(bf16x8 p, int i, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 v = {p[2 * i], p[2 * i + 1]};
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
+}
+__device__ __forceinline__ float dot2_ones(f16x8 p, int i, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = {p[2 * i], p[2 * i + 1]};
+  const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(v, one, acc, false);
+}
+
+template <typename T, int D, int BKV, int NT, int STAGES, int WAVES, bool ALIBI>
+__global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const PrefillParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
-  typedef Tile<D, BKV> TL;
+  typedef TileGeom<D, BKV, WAVES> TG;
   constexpr int MT = BKV / 32;   // 32-key row tiles of S^T
   constexpr int KS = D / 16;     // k-steps of QK^T
   constexpr int MD = D / 32;     // 32-wide head-dim tiles of O^T
   constexpr int KS2 = BKV / 16;  // k-steps of PV
-  constexpr int THREADS = kWaves * 64;
+  static_assert(MT >= 1 && STAGES >= 3, "tile shape");
 
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* smem = reinterpret_cast<T*>(smem_raw);
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const goda_prefill_args& a = p.a;
   const int hg = p.heads_per_wg;
   const int nslices = p.group / hg;
-  const int qb_rows = (kWaves / hg) * 32 * NT;  // query rows per workgroup
+  const int qb_rows = (WAVES / hg) * 32 * NT;  // query rows per workgroup
   const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
 
-  // XCD-aware order: consecutive dispatch slots rotate over the 8 XCDs; give
-  // each XCD a contiguous range of (sequence, head-slice) pairs so that the
+  // XCD-aware order: consecutive dispatch slots rotate over the 8 XCDs; each
+  // XCD gets a contiguous range of (sequence, head-slice) pairs so the
   // workgroups sharing K/V tiles share that XCD's L2. Heavy causal query
   // tiles go first.
   const int nblk = gridDim.x;
@@ -190,7 +269,7 @@ __global__ void __launch_bounds__(kWaves * 64, 1) prefill_mfma_kernel(const Pref
   const int diag = g.lk - g.lq;
   const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
 
-  // ---- Q^T operand fragments (rotated) -------------------------------------
+  // ---- Q^T operand fragments (rotated) ---------------------------------------
   v8 qf[NT][KS];
   {
     const T* qbase = reinterpret_cast<const T*>(a.q) +
@@ -237,42 +316,6 @@ __global__ void __launch_bounds__(kWaves * 64, 1) prefill_mfma_kernel(const Pref
   const int j_lo = kv_lo / BKV;
   const int j_hi = kv_hi > 0 ? (kv_hi + BKV - 1) / BKV : 0;
 
-  const T* kp = reinterpret_cast<const T*>(a.workspace);
-  const int64_t tile_elems = (int64_t)BKV * D;
-  const int64_t ntot = (int64_t)a.batch * p.ntiles_k * a.heads_kv;
-  const T* vt = kp + ntot * tile_elems;
-
-  // Global -> register staging of one K'/V^T tile pair.
-  constexpr int NVEC = BKV * D / 8 / THREADS;  // 16-byte vectors per thread per tensor
-  static_assert(NVEC >= 1 && (BKV * D / 8) % THREADS == 0, "tile not divisible");
-  v8 kreg[NVEC], vreg[NVEC];
-  auto load_tile = [&](int j) {
-    const int64_t t = ws_tile(b, j, hk, p.ntiles_k, a.heads_kv);
-    const T* ks = kp + t * tile_elems;
-    const T* vs = vt + t * tile_elems;
-#pragma unroll
-    for (int i = 0; i < NVEC; ++i) {
-      const int v = tid + i * THREADS;
-      kreg[i] = ld_vec<v8>(ks + v * 8);
-      vreg[i] = ld_vec<v8>(vs + v * 8);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    T* kl = smem + buf * TL::STAGE_ELEMS;
-    T* vl = kl + TL::K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < NVEC; ++i) {
-      const int v = tid + i * THREADS;
-      const int kr = v / (D / 8), kc = (v % (D / 8)) * 8;
-      st_vec<v8>(kl + kr * TL::KLD + kc, kreg[i]);
-      const int vr = v / (BKV / 8), vc = (v % (BKV / 8)) * 8;
-      const v4 lo = {vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3]};
-      const v4 hi4 = {vreg[i][4], vreg[i][5], vreg[i][6], vreg[i][7]};
-      st_vec<v4>(vl + vr * TL::VLD + vc, lo);
-      st_vec<v4>(vl + vr * TL::VLD + vc + 4, hi4);
-    }
-  };
-
   f32x16 oacc[MD][NT];
 #pragma unroll
   for (int md = 0; md < MD; ++md)
@@ -287,100 +330,156 @@ __global__ void __launch_bounds__(kWaves * 64, 1) prefill_mfma_kernel(const Pref
   const float c = p.scale_log2;
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
 
-  if (j_lo < j_hi) {
-    load_tile(j_lo);
-    store_tile(0);
-  }
-  __syncthreads();
+  // ---- tile DMA ---------------------------------------------------------------
+  const unsigned char* ws = reinterpret_cast<const unsigned char*>(a.workspace);
+  auto dma = [&](int j) {
+    const unsigned char* src = ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES +
+                               (wave * TG::DMA_PER_WAVE * 64 + lane) * 16;
+    unsigned char* dst = smem + (j % STAGES) * TG::BYTES + wave * TG::DMA_PER_WAVE * 64 * 16;
+#pragma unroll
+    for (int i = 0; i < TG::DMA_PER_WAVE; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(src + i * 1024),
+                                       (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0,
+                                       0);
+  };
 
-  for (int j = j_lo; j < j_hi; ++j) {
-    const int buf = (j - j_lo) & 1;
-    if (j + 1 < j_hi) load_tile(j + 1);
-    const T* kl = smem + buf * TL::STAGE_ELEMS;
-    const T* vl = kl + TL::K_ELEMS;
-
-    // S^T = K' Q^T
-    f32x16 sacc[MT][NT];
+  // This lane's K' operand for (ks, mt) is chunk (2ks + hi)*BKV + 32mt + l32;
+  // its V^T operand for (ks2, md) is chunk (2ks2 + hi)*D + 32md + l32.
+  auto qk = [&](int j, f32x16 (&s)[MT][NT]) {
+    const v8* kp = reinterpret_cast<const v8*>(smem + (j % STAGES) * TG::BYTES) + hi * BKV + l32;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) sacc[mt][nt] = f32x16{};
+      for (int nt = 0; nt < NT; ++nt) s[mt][nt] = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const v8 av = ld_vec<v8>(kl + (32 * mt + l32) * TL::KLD + 16 * ks + 8 * hi);
+        const v8 av = kp[ks * 2 * BKV + mt * 32];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) sacc[mt][nt] = mfma32(av, qf[nt][ks], sacc[mt][nt]);
+        for (int nt = 0; nt < NT; ++nt) s[mt][nt] = mfma32(av, qf[nt][ks], s[mt][nt]);
       }
-    }
+  };
 
-    // Mask, online softmax, P^T fragments.
+  // One pipelined step: consumes the scores s_in of tile j, issues the scores
+  // of tile j+1 into s_out, accumulates P(j)V(j).
+  auto step = [&](int j, f32x16 (&s_in)[MT][NT], f32x16 (&s_out)[MT][NT]) {
+    const bool has_next = j + 1 < j_hi;
+    // Tile j+1 must be resident before S(j+1) is formed: wait for every DMA
+    // group except the newer tiles j+2 .. j+STAGES-2 already issued.
+    if (has_next) wait_dma_groups<TG::DMA_PER_WAVE, STAGES - 3>(min(STAGES - 3, j_hi - j - 2));
+    // After this barrier no wave reads the stage of tile j-1 any more.
+    __syncthreads();
+    if (j + STAGES - 1 < j_hi) dma(j + STAGES - 1);
+
+    // ---- scores of tile j in the scaled log2 domain -------------------------------
     const int kvb = j * BKV;
-    const bool need_mask = (kvb + BKV > g.lk) ||
-                           (a.causal && kvb + BKV - 1 > diag + wrow0) ||
+    const bool need_mask = (kvb + BKV > g.lk) || (a.causal && kvb + BKV - 1 > diag + wrow0) ||
                            (use_window && kvb < diag + wrow0 + 32 * NT - 1 - a.window_left);
-    v8 pf[NT][KS2];
+    if (ALIBI || need_mask) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int qi = wrow0 + 32 * nt + l32;
-      const int iabs = diag + qi;
-      if (need_mask || ALIBI) {
+      for (int nt = 0; nt < NT; ++nt) {
+        const int iabs = diag + wrow0 + 32 * nt + l32;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int kv = kvb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-            bool vis = kv < g.lk;
-            if (a.causal) vis = vis && kv <= iabs;
-            if (use_window) vis = vis && (iabs - kv <= a.window_left);
-            float t = sacc[mt][nt][r];
+            float t = s_in[mt][nt][r];
             if (ALIBI) t = fmaf(t, c, slope2 * (float)(kv - iabs));
-            sacc[mt][nt][r] = vis ? t : kNegInf;
+            if (need_mask) {
+              bool vis = kv < g.lk;
+              if (a.causal) vis = vis && kv <= iabs;
+              if (use_window) vis = vis && (iabs - kv <= a.window_left);
+              t = vis ? t : kNegInf;
+            }
+            s_in[mt][nt][r] = t;
           }
       }
+    }
+
+    // ---- row max and lazy rescale ---------------------------------------------------
+    float mtile[NT];
+    bool grow = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
       float mx = kNegInf;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[mt][nt][r]);
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      const float m_new = fmaxf(m_run[nt], ALIBI ? mx : mx * c);
-      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[nt] - m_use);
-      m_run[nt] = m_new;
-      float lsum = 0.f;
+        for (int r = 0; r < 16; r += 2) mx = max3f(mx, s_in[mt][nt][r], s_in[mt][nt][r + 1]);
+      mx = half_max(mx);
+      mtile[nt] = ALIBI ? mx : mx * c;
+      grow = grow || (mtile[nt] > m_run[nt] + kRescaleThresh);
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float mn = fmaxf(m_run[nt], mtile[nt]);
+        const float alpha = (m_run[nt] == kNegInf) ? 0.f : fast_exp2(m_run[nt] - mn);
+        m_run[nt] = mn;
+        l_run[nt] *= alpha;
+#pragma unroll
+        for (int md = 0; md < MD; ++md) oacc[md][nt] *= alpha;
+      }
+    }
+
+    // ---- S(j+1) on the MFMA pipe while P(j) is formed on the VALU -------------------
+    // Issued unconditionally (the last step recomputes tile j, whose result is
+    // unused) so the MFMAs and the softmax VALU work share one basic block.
+    qk(has_next ? j + 1 : j, s_out);
+
+    v8 pf[NT][KS2];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float m_use = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];
+      float lsum = l_run[nt];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float s = sacc[mt][nt][r];
-          const float pv = ALIBI ? fast_exp2(s - m_use) : fast_exp2(fmaf(s, c, -m_use));
-          lsum += pv;
-          pf[nt][2 * mt + (r >> 3)][r & 7] = (T)pv;
+        for (int h = 0; h < 2; ++h) {
+          v8 pv;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float s = s_in[mt][nt][8 * h + e];
+            pv[e] = (T)(ALIBI ? fast_exp2(s - m_use) : fast_exp2(fmaf(s, c, -m_use)));
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) lsum = dot2_ones(pv, i, lsum);
+          pf[nt][2 * mt + h] = pv;
         }
       }
-      l_run[nt] = l_run[nt] * alpha + lsum;
-#pragma unroll
-      for (int md = 0; md < MD; ++md) oacc[md][nt] *= alpha;
+      l_run[nt] = lsum;
     }
 
-    // O^T += V^T P^T
+    // ---- O^T += V^T P^T --------------------------------------------------------------
+    const v8* vp = reinterpret_cast<const v8*>(smem + (j % STAGES) * TG::BYTES + TG::K_CHUNKS * 16) +
+                   hi * D + l32;
 #pragma unroll
-    for (int ks2 = 0; ks2 < KS2; ++ks2) {
+    for (int ks2 = 0; ks2 < KS2; ++ks2)
 #pragma unroll
       for (int md = 0; md < MD; ++md) {
-        const T* vp = vl + (32 * md + l32) * TL::VLD + 16 * ks2 + 4 * hi;
-        const v4 a0 = ld_vec<v4>(vp);
-        const v4 a1 = ld_vec<v4>(vp + 8);
-        const v8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const v8 av = vp[ks2 * 2 * D + md * 32];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) oacc[md][nt] = mfma32(av, pf[nt][ks2], oacc[md][nt]);
       }
-    }
+  };
 
-    if (j + 1 < j_hi) store_tile(buf ^ 1);
+  // ---- prologue: first STAGES-1 tiles in flight, scores of tile j_lo -----------------
+  const int ntile = j_hi - j_lo;
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ntile) dma(j_lo + t);
+  f32x16 s_a[MT][NT], s_b[MT][NT];
+  if (ntile > 0) {
+    wait_dma_groups<TG::DMA_PER_WAVE, STAGES - 2>(min(STAGES - 1, ntile) - 1);
     __syncthreads();
+    qk(j_lo, s_a);
+  }
+  // Unrolled by two so the score buffers alternate without register copies.
+  for (int j = j_lo; j < j_hi; j += 2) {
+    step(j, s_a, s_b);
+    if (j + 1 < j_hi) step(j + 1, s_b, s_a);
   }
 
   // ---- epilogue ------------------------------------------------------------
@@ -388,7 +487,7 @@ __global__ void __launch_bounds__(kWaves * 64, 1) prefill_mfma_kernel(const Pref
              (int64_t)hq * a.o_stride_h;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const float ltot = l_run[nt] + shfl_xor_f(l_run[nt], 32);
+    const float ltot = half_sum(l_run[nt]);
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
     const int qi = wrow0 + 32 * nt + l32;
     if (qi < g.lq) {
@@ -416,8 +515,25 @@ __global__ void __launch_bounds__(kWaves * 64, 1) prefill_mfma_kernel(const Pref
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-int kv_tile_for(int d) { return 64; }
-int nt_for(int d) { return d >= 256 ? 1 : 2; }
+// Tile shape per head dim: keys per tile, 32-row query tiles per wave, ring
+// depth, waves per workgroup (8 = two per SIMD, so one wave's MFMAs overlap
+// the other's softmax; 4 when a wave needs more than half the register file).
+template <int D>
+struct Config;
+template <>
+struct Config<64> {
+  static constexpr int BKV = 64, NT = 1, STAGES = 4, WAVES = 8;
+};
+template <>
+struct Config<128> {
+  static constexpr int BKV = 64, NT = 1, STAGES = 3, WAVES = 8;
+};
+template <>
+struct Config<256> {
+  static constexpr int BKV = 32, NT = 1, STAGES = 3, WAVES = 4;
+};
+
+int kv_tile_for(int d) { return d >= 256 ? Config<256>::BKV : d >= 128 ? Config<128>::BKV : Config<64>::BKV; }
 
 int gcd_int(int x, int y) {
   while (y) {
@@ -428,30 +544,31 @@ int gcd_int(int x, int y) {
   return x;
 }
 
-template <typename T, int D, int BKV, int NT, bool ALIBI>
+template <typename T, int D, bool ALIBI>
 hipError_t launch_attn(PrefillParams p, hipStream_t s) {
+  typedef Config<D> C;
   const goda_prefill_args& a = p.a;
-  const int hg = gcd_int(p.group, kWaves);
+  const int hg = gcd_int(p.group, C::WAVES);
   p.heads_per_wg = hg;
-  const int qb_rows = (kWaves / hg) * 32 * NT;
+  const int qb_rows = (C::WAVES / hg) * 32 * C::NT;
   const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
   const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / hg);
   if (nblk <= 0) return hipSuccess;
   if (nblk > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t lds = 2 * Tile<D, BKV>::STAGE_ELEMS * sizeof(T);
-  auto kern = prefill_mfma_kernel<T, D, BKV, NT, ALIBI>;
+  const size_t lds = (size_t)C::STAGES * TileGeom<D, C::BKV, C::WAVES>::BYTES;
+  auto kern = prefill_fa_kernel<T, D, C::BKV, C::NT, C::STAGES, C::WAVES, ALIBI>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
   if ((e = record_timing(a.timing_begin, s)) != hipSuccess) return e;
-  kern<<<dim3((unsigned)nblk), dim3(kWaves * 64), lds, s>>>(p);
+  kern<<<dim3((unsigned)nblk), dim3(C::WAVES * 64), lds, s>>>(p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   return record_timing(a.timing_end, s);
 }
 
 template <typename T, int D>
 hipError_t launch_d(PrefillParams p, hipStream_t s) {
-  constexpr int BKV = 64;
+  constexpr int BKV = Config<D>::BKV;
   const goda_prefill_args& a = p.a;
   p.kv_tile = BKV;
   p.ntiles_k = (a.seqlen_k + BKV - 1) / BKV;
@@ -461,9 +578,8 @@ hipError_t launch_d(PrefillParams p, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  constexpr int NT = D >= 256 ? 1 : 2;
-  if (a.alibi_slopes) return launch_attn<T, D, BKV, NT, true>(p, s);
-  return launch_attn<T, D, BKV, NT, false>(p, s);
+  if (a.alibi_slopes) return launch_attn<T, D, true>(p, s);
+  return launch_attn<T, D, false>(p, s);
 }
 
 template <typename T>
