@@ -30,6 +30,9 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    # The kernels type-pun through vector pointers (element arrays read as
+    # 16-byte vectors and back); keep type-based alias analysis out of it.
+    "-fno-strict-aliasing",
     "-Xclang",
     "-target-feature",
     "-Xclang",

@@ -14,12 +14,15 @@
 //      Inside each 16-key group of the V^T image the keys are stored in the
 //      order the P^T register fragment holds them (kPermKey), so one 16-byte
 //      read yields a whole MFMA operand.
-//   2. prefill_fa_kernel: one workgroup (4 waves, one per SIMD) per (query
-//      tile, query-head slice, sequence). All waves belong to query heads of
-//      ONE KV head, so every K/V tile streamed into LDS serves the whole
-//      query-head group ("read once per group"). Tiles arrive by direct
-//      global->LDS DMA (global_load_lds_dwordx4) into a ring of STAGES
-//      buffers, STAGES-1 tiles ahead of use.
+//   2. prefill_fa_kernel: one workgroup (8 waves, two per SIMD; 4 for
+//      D = 256) per (query tile, query-head slice, sequence). All waves
+//      belong to query heads of ONE KV head, so every K/V tile streamed into
+//      LDS serves the whole query-head group ("read once per group"). Tiles
+//      move through a ring of 3 LDS stages: during the interval that reads
+//      tiles j and j+1, each wave loads its share of tile j+2 into registers
+//      and writes it to the free stage at the end. (Direct global->LDS DMA
+//      would save those registers, but while such a load is in flight the
+//      compiler waits for ALL LDS reads before every MFMA operand use.)
 //
 // Per wave and KV tile (32x32x16 MFMA, 32*NT query rows of one head):
 //   S^T[kv][q] = K'[kv][d] . Q^T[d][q]     A = K' (LDS), B = Q^T (registers)
@@ -69,34 +72,22 @@ struct TileGeom {
   static constexpr int K_CHUNKS = D / 8 * BKV;  // 16-byte chunks of the K' image
   static constexpr int V_CHUNKS = BKV / 8 * D;
   static constexpr int BYTES = (K_CHUNKS + V_CHUNKS) * 16;
-  static constexpr int DMA_PER_WAVE = (K_CHUNKS + V_CHUNKS) / (64 * WAVES);
+  static constexpr int LOADS_PER_LANE = (K_CHUNKS + V_CHUNKS) / (64 * WAVES);  // 16-byte loads
   static_assert((K_CHUNKS + V_CHUNKS) % (64 * WAVES) == 0, "tile must split evenly over the waves");
 };
+constexpr int kStages = 3;  // LDS ring: tiles j, j+1 read, tile j+2 written
 
 // Index of workspace tile j of sequence b, KV head hk.
 __device__ __forceinline__ int64_t ws_tile(int b, int j, int hk, int ntiles, int hkv) {
   return ((int64_t)b * ntiles + j) * hkv + hk;
 }
 
-// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-// Wait until at most `groups` DMA groups of PER instructions are in flight.
-template <int PER, int MAXG>
-__device__ __forceinline__ void wait_dma_groups(int groups) {
-  if constexpr (MAXG > 0) {
-    if (groups >= MAXG) {
-      wait_vmcnt<MAXG * PER>();
-      return;
-    }
-    wait_dma_groups<PER, MAXG - 1>(groups);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
+// Workgroup barrier for the tile ring. __syncthreads() would also wait for
+// every outstanding global access (vmcnt(0)), i.e. for the registers of the
+// tile being prefetched; the ring only needs this wave's LDS accesses
+// retired. The "memory" clobber keeps the compiler from moving LDS accesses
+// across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
 // 1. pack K (rotated) and V^T into tile images
@@ -221,7 +212,7 @@ __device__ __forceinline__ float dot2_ones(f16x8 p, int i, float acc) {
   return __builtin_amdgcn_fdot2(v, one, acc, false);
 }
 
-template <typename T, int D, int BKV, int NT, int STAGES, int WAVES, bool ALIBI>
+template <typename T, int D, int BKV, int NT, int WAVES, bool ALIBI>
 __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const PrefillParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
@@ -230,7 +221,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   constexpr int KS = D / 16;     // k-steps of QK^T
   constexpr int MD = D / 32;     // 32-wide head-dim tiles of O^T
   constexpr int KS2 = BKV / 16;  // k-steps of PV
-  static_assert(MT >= 1 && STAGES >= 3, "tile shape");
+  static_assert(MT >= 1, "tile shape");
 
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -305,6 +296,13 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = v8{};
       }
     }
+    // Pin the fragments in registers: without this the compiler treats the
+    // (read-only) q loads as rematerializable and re-reads q from global
+    // memory inside the key loop.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qf[nt][ks]));
   }
 
   // ---- key tile range ---------------------------------------------------------
@@ -330,23 +328,30 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   const float c = p.scale_log2;
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
 
-  // ---- tile DMA ---------------------------------------------------------------
+  // ---- tile ring ----------------------------------------------------------------
+  // Lane chunk c of this wave's share sits at the same offset in the
+  // workspace tile and in the LDS stage.
+  constexpr int LOADS = TG::LOADS_PER_LANE;
   const unsigned char* ws = reinterpret_cast<const unsigned char*>(a.workspace);
-  auto dma = [&](int j) {
-    const unsigned char* src = ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES +
-                               (wave * TG::DMA_PER_WAVE * 64 + lane) * 16;
-    unsigned char* dst = smem + (j % STAGES) * TG::BYTES + wave * TG::DMA_PER_WAVE * 64 * 16;
+  const int my_chunk0 = wave * LOADS * 64 + lane;
+  // (Stored and later read through the same operand type v8.)
+  v8 stg[LOADS];
+  auto tile_load = [&](int j) {
+    const v8* src = reinterpret_cast<const v8*>(ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES) +
+                    my_chunk0;
 #pragma unroll
-    for (int i = 0; i < TG::DMA_PER_WAVE; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(src + i * 1024),
-                                       (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0,
-                                       0);
+    for (int i = 0; i < LOADS; ++i) stg[i] = src[i * 64];
+  };
+  auto tile_store = [&](int j) {
+    v8* dst = reinterpret_cast<v8*>(smem + (j % kStages) * TG::BYTES) + my_chunk0;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) dst[i * 64] = stg[i];
   };
 
   // This lane's K' operand for (ks, mt) is chunk (2ks + hi)*BKV + 32mt + l32;
   // its V^T operand for (ks2, md) is chunk (2ks2 + hi)*D + 32md + l32.
   auto qk = [&](int j, f32x16 (&s)[MT][NT]) {
-    const v8* kp = reinterpret_cast<const v8*>(smem + (j % STAGES) * TG::BYTES) + hi * BKV + l32;
+    const v8* kp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES) + hi * BKV + l32;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -361,18 +366,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       }
   };
 
-  // One pipelined step: consumes the scores s_in of tile j, issues the scores
-  // of tile j+1 into s_out, accumulates P(j)V(j).
-  auto step = [&](int j, f32x16 (&s_in)[MT][NT], f32x16 (&s_out)[MT][NT]) {
-    const bool has_next = j + 1 < j_hi;
-    // Tile j+1 must be resident before S(j+1) is formed: wait for every DMA
-    // group except the newer tiles j+2 .. j+STAGES-2 already issued.
-    if (has_next) wait_dma_groups<TG::DMA_PER_WAVE, STAGES - 3>(min(STAGES - 3, j_hi - j - 2));
-    // After this barrier no wave reads the stage of tile j-1 any more.
-    __syncthreads();
-    if (j + STAGES - 1 < j_hi) dma(j + STAGES - 1);
-
-    // ---- scores of tile j in the scaled log2 domain -------------------------------
+  // ---- softmax half of a step: scores s of tile j -> probabilities pf --------------
+  auto vpart = [&](int j, f32x16 (&s)[MT][NT], v8 (&pf)[NT][KS2]) {
     const int kvb = j * BKV;
     const bool need_mask = (kvb + BKV > g.lk) || (a.causal && kvb + BKV - 1 > diag + wrow0) ||
                            (use_window && kvb < diag + wrow0 + 32 * NT - 1 - a.window_left);
@@ -385,7 +380,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int kv = kvb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-            float t = s_in[mt][nt][r];
+            float t = s[mt][nt][r];
             if (ALIBI) t = fmaf(t, c, slope2 * (float)(kv - iabs));
             if (need_mask) {
               bool vis = kv < g.lk;
@@ -393,12 +388,11 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
               if (use_window) vis = vis && (iabs - kv <= a.window_left);
               t = vis ? t : kNegInf;
             }
-            s_in[mt][nt][r] = t;
+            s[mt][nt][r] = t;
           }
       }
     }
-
-    // ---- row max and lazy rescale ---------------------------------------------------
+    // row max and lazy rescale
     float mtile[NT];
     bool grow = false;
 #pragma unroll
@@ -407,7 +401,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) mx = max3f(mx, s_in[mt][nt][r], s_in[mt][nt][r + 1]);
+        for (int r = 0; r < 16; r += 2) mx = max3f(mx, s[mt][nt][r], s[mt][nt][r + 1]);
       mx = half_max(mx);
       mtile[nt] = ALIBI ? mx : mx * c;
       grow = grow || (mtile[nt] > m_run[nt] + kRescaleThresh);
@@ -423,13 +417,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         for (int md = 0; md < MD; ++md) oacc[md][nt] *= alpha;
       }
     }
-
-    // ---- S(j+1) on the MFMA pipe while P(j) is formed on the VALU -------------------
-    // Issued unconditionally (the last step recomputes tile j, whose result is
-    // unused) so the MFMAs and the softmax VALU work share one basic block.
-    qk(has_next ? j + 1 : j, s_out);
-
-    v8 pf[NT][KS2];
+    // probabilities (rounded to the operand type) and their row sums
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const float m_use = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];
@@ -441,8 +429,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
           v8 pv;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float s = s_in[mt][nt][8 * h + e];
-            pv[e] = (T)(ALIBI ? fast_exp2(s - m_use) : fast_exp2(fmaf(s, c, -m_use)));
+            const float x = s[mt][nt][8 * h + e];
+            pv[e] = (T)(ALIBI ? fast_exp2(x - m_use) : fast_exp2(fmaf(x, c, -m_use)));
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) lsum = dot2_ones(pv, i, lsum);
@@ -451,9 +439,11 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       }
       l_run[nt] = lsum;
     }
+  };
 
-    // ---- O^T += V^T P^T --------------------------------------------------------------
-    const v8* vp = reinterpret_cast<const v8*>(smem + (j % STAGES) * TG::BYTES + TG::K_CHUNKS * 16) +
+  // ---- O^T += V^T P^T for tile j ----------------------------------------------------
+  auto pv_mfma = [&](int j, const v8 (&pf)[NT][KS2]) {
+    const v8* vp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES + TG::K_CHUNKS * 16) +
                    hi * D + l32;
 #pragma unroll
     for (int ks2 = 0; ks2 < KS2; ++ks2)
@@ -465,21 +455,91 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       }
   };
 
-  // ---- prologue: first STAGES-1 tiles in flight, scores of tile j_lo -----------------
-  const int ntile = j_hi - j_lo;
+  // MFMA half of a step: O += P(j)V(j), then S(j+1) = K(j+1)Q^T (tile j again,
+  // result unused, on the last step so the phase stays one basic block).
+  // The schedule keeps the LDS operand reads kLead MFMAs ahead of their use,
+  // so each wave's MFMA phase runs back to back instead of waiting out an
+  // LDS round trip every two MFMAs.
+  auto mphase = [&](int j, const v8 (&pf)[NT][KS2], f32x16 (&s)[MT][NT]) {
+    pv_mfma(j, pf);
+    qk(j + 1 < j_hi ? j + 1 : j, s);
+    constexpr int kMfma = KS2 * MD * NT + KS * MT * NT;
+    constexpr int kReads = KS2 * MD + KS * MT;
+    constexpr int kLead = 4;
+    static_assert(kReads > kLead, "phase too short");
+    __builtin_amdgcn_sched_group_barrier(0x100, kLead, 0);
 #pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t)
-    if (t < ntile) dma(j_lo + t);
-  f32x16 s_a[MT][NT], s_b[MT][NT];
+    for (int i = 0; i < kReads - kLead; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, kMfma / kReads, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kLead * (kMfma / kReads), 0);
+  };
+
+  // Start of the ring interval that reads tiles j (V) and j+1 (K). Past the
+  // barrier, tile j+1 (written at the end of the previous interval) is
+  // visible and nobody reads the stage of tile j-1, which tile j+2 takes over
+  // at the end of this interval; its global loads are issued now.
+  auto ring_begin = [&](int j) {
+    ring_barrier();
+    if (j + 2 < j_hi) tile_load(j + 2);
+  };
+  auto ring_end = [&](int j) {
+    if (j + 2 < j_hi) tile_store(j + 2);
+  };
+
+  // ---- prologue: tiles j_lo and j_lo+1 resident, scores of tile j_lo ------------------
+  const int ntile = j_hi - j_lo;
+  f32x16 s_a[MT][NT];
+  v8 pf[NT][KS2];
   if (ntile > 0) {
-    wait_dma_groups<TG::DMA_PER_WAVE, STAGES - 2>(min(STAGES - 1, ntile) - 1);
-    __syncthreads();
+    tile_load(j_lo);
+    tile_store(j_lo);
+    if (ntile > 1) {
+      tile_load(j_lo + 1);
+      tile_store(j_lo + 1);
+    }
+    ring_barrier();
     qk(j_lo, s_a);
   }
-  // Unrolled by two so the score buffers alternate without register copies.
-  for (int j = j_lo; j < j_hi; j += 2) {
-    step(j, s_a, s_b);
-    if (j + 1 < j_hi) step(j + 1, s_b, s_a);
+
+  if constexpr (WAVES == 8) {
+    // Two waves share each SIMD (waves w and w+4). They run the same
+    // sequence of tiles half an interval apart, so one wave's MFMA work
+    // (P(j)V(j) and S(j+1)) overlaps the other's softmax:
+    //   group 0: | softmax(j)  MFMA(j)       | softmax(j+1) MFMA(j+1) | ...
+    //   group 1: | MFMA(j)     softmax(j+1)  | MFMA(j+1)    ...
+    // Both groups touch tiles j and j+1 in interval j, so the ring is the
+    // same for both.
+    if (wave >= 4 && ntile > 0) vpart(j_lo, s_a, pf);
+    for (int j = j_lo; j < j_hi; ++j) {
+      ring_begin(j);
+      if (wave < 4) {
+        vpart(j, s_a, pf);
+        mphase(j, pf, s_a);
+      } else {
+        mphase(j, pf, s_a);
+        if (j + 1 < j_hi) vpart(j + 1, s_a, pf);
+      }
+      ring_end(j);
+    }
+  } else {
+    // One wave per SIMD: overlap inside the wave instead. The MFMAs of
+    // S(j+1) are issued in the same basic block as the softmax VALU work on
+    // S(j) (unconditionally: the last step recomputes tile j and drops it).
+    f32x16 s_b[MT][NT];
+    auto step = [&](int j, f32x16 (&s_in)[MT][NT], f32x16 (&s_out)[MT][NT]) {
+      ring_begin(j);
+      qk(j + 1 < j_hi ? j + 1 : j, s_out);
+      vpart(j, s_in, pf);
+      pv_mfma(j, pf);
+      ring_end(j);
+    };
+    // Unrolled by two so the score buffers alternate without register copies.
+    for (int j = j_lo; j < j_hi; j += 2) {
+      step(j, s_a, s_b);
+      if (j + 1 < j_hi) step(j + 1, s_b, s_a);
+    }
   }
 
   // ---- epilogue ------------------------------------------------------------
@@ -515,22 +575,22 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-// Tile shape per head dim: keys per tile, 32-row query tiles per wave, ring
-// depth, waves per workgroup (8 = two per SIMD, so one wave's MFMAs overlap
-// the other's softmax; 4 when a wave needs more than half the register file).
+// Tile shape per head dim: keys per tile, 32-row query tiles per wave, waves
+// per workgroup (8 = two per SIMD, so one wave's MFMAs overlap the other's
+// softmax; 4 when a wave needs more than half the register file).
 template <int D>
 struct Config;
 template <>
 struct Config<64> {
-  static constexpr int BKV = 64, NT = 1, STAGES = 4, WAVES = 8;
+  static constexpr int BKV = 64, NT = 1, WAVES = 8;
 };
 template <>
 struct Config<128> {
-  static constexpr int BKV = 64, NT = 1, STAGES = 3, WAVES = 8;
+  static constexpr int BKV = 64, NT = 1, WAVES = 8;
 };
 template <>
 struct Config<256> {
-  static constexpr int BKV = 32, NT = 1, STAGES = 3, WAVES = 4;
+  static constexpr int BKV = 32, NT = 1, WAVES = 4;
 };
 
 int kv_tile_for(int d) { return d >= 256 ? Config<256>::BKV : d >= 128 ? Config<128>::BKV : Config<64>::BKV; }
@@ -555,8 +615,8 @@ hipError_t launch_attn(PrefillParams p, hipStream_t s) {
   const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / hg);
   if (nblk <= 0) return hipSuccess;
   if (nblk > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t lds = (size_t)C::STAGES * TileGeom<D, C::BKV, C::WAVES>::BYTES;
-  auto kern = prefill_fa_kernel<T, D, C::BKV, C::NT, C::STAGES, C::WAVES, ALIBI>;
+  const size_t lds = (size_t)kStages * TileGeom<D, C::BKV, C::WAVES>::BYTES;
+  auto kern = prefill_fa_kernel<T, D, C::BKV, C::NT, C::WAVES, ALIBI>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
