@@ -1,0 +1,3 @@
+from .base import KVCache
+
+__all__ = ["KVCache"]

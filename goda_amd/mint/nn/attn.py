@@ -1,0 +1,118 @@
+"""goda's attention layers (mint/nn/attn.py:10-145) on the HIP kernels.
+
+Same constructors and `forward(x, kv_cache, start_pos, base_attn_mask,
+doc_ids)`. The difference is where the positional encoding happens: a RoPE
+or ALiBi `pos_embeddings` from `goda_amd.mint.nn.pos` is fused into the
+attention kernels (q and k are rotated while the kernels stage them; ALiBi is
+added to the scores) instead of running as separate elementwise passes, and
+ALiBi is actually applied (the reference asserts it away, mint/nn/attn.py:62).
+Any other `pos_embeddings` module is called as in the reference and must not
+return a bias.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from ..kvcache.base import KVCache
+from .flashattn import FlashAttention
+from .pos import ALiBiPositionalBias, RoPE
+
+
+class RMSNorm(nn.Module):
+    """mint/nn/norm.py:10-27: fp32 RMS norm with (1 + scale), scale zero-initialised."""
+
+    def __init__(self, emb_dim: int, eps: float = 1e-6, *, bias: bool = False) -> None:
+        super().__init__()
+        self.eps = eps
+        self.scale = nn.Parameter(torch.zeros(emb_dim))
+        self.shift = nn.Parameter(torch.zeros(emb_dim)) if bias else None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x_f = x.float()
+        var = x_f.pow(2).mean(dim=-1, keepdim=True)
+        out = x_f * torch.rsqrt(var + self.eps) * (1.0 + self.scale.float())
+        if self.shift is not None:
+            out = out + self.shift.float()
+        return out.to(x.dtype)
+
+
+class GroupedQueryAttention(nn.Module):
+    def __init__(
+        self,
+        n_heads: int,
+        n_kv_heads: int,
+        head_dim: int,
+        embed_dim: int,
+        pos_embeddings: nn.Module,
+        dtype: torch.dtype,
+        window_size: int = -1,
+    ) -> None:
+        super().__init__()
+        self.n_heads = n_heads
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.window_size = window_size
+        self.pos_embeddings = pos_embeddings
+        self.attention = FlashAttention(use_custom_fa=True)
+        self.wq = nn.Linear(embed_dim, n_heads * head_dim, bias=False, dtype=dtype)
+        self.wk = nn.Linear(embed_dim, n_kv_heads * head_dim, bias=False, dtype=dtype)
+        self.wv = nn.Linear(embed_dim, n_kv_heads * head_dim, bias=False, dtype=dtype)
+        self.wo = nn.Linear(n_heads * head_dim, embed_dim, bias=False, dtype=dtype)
+        self.q_norm = RMSNorm(head_dim)
+        self.k_norm = RMSNorm(head_dim)
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        kv_cache: KVCache | None = None,
+        start_pos: int = 0,
+        base_attn_mask: torch.Tensor = None,
+        doc_ids: torch.Tensor = None,
+    ) -> torch.Tensor:
+        bsz, seqlen, _ = x.shape
+        q = self.wq(x).view(bsz, seqlen, self.n_heads, self.head_dim)
+        k = self.wk(x).view(bsz, seqlen, self.n_kv_heads, self.head_dim)
+        v = self.wv(x).view(bsz, seqlen, self.n_kv_heads, self.head_dim)
+        q = self.q_norm(q)
+        k = self.k_norm(k)
+
+        fused: dict = {}
+        if isinstance(self.pos_embeddings, RoPE):
+            fused = {"rope": (self.pos_embeddings.cos, self.pos_embeddings.sin), "start_pos": start_pos}
+        elif isinstance(self.pos_embeddings, ALiBiPositionalBias):
+            fused = {"alibi_slopes": self.pos_embeddings.slopes}
+        else:
+            q, k, attn_bias = self.pos_embeddings(q, k, start_pos=start_pos)
+            if attn_bias is not None:
+                raise NotImplementedError("goda_amd: only RoPE / ALiBi biases are fused")
+
+        window_size = (self.window_size, -1) if self.window_size > 0 else (-1, -1)
+        out = self.attention(
+            q,
+            k,
+            v,
+            causal=True,
+            window_size=window_size,
+            kv_cache=kv_cache,
+            base_attn_mask=base_attn_mask,
+            doc_ids=doc_ids,
+            **fused,
+        )
+        return self.wo(out.reshape(bsz, seqlen, -1))
+
+
+class MultiHeadAttention(GroupedQueryAttention):
+    """mint/nn/attn.py:80-145: GQA with n_kv_heads == n_heads."""
+
+    def __init__(
+        self,
+        n_heads: int,
+        head_dim: int,
+        embed_dim: int,
+        pos_embeddings: nn.Module,
+        dtype: torch.dtype,
+        window_size: int = -1,
+    ) -> None:
+        super().__init__(n_heads, n_heads, head_dim, embed_dim, pos_embeddings, dtype, window_size)

@@ -1,0 +1,144 @@
+"""Drop-in for goda's attention dispatcher (mint/nn/flashattn.py:14-273),
+backed entirely by the HIP kernels.
+
+`FlashAttention.forward(q, k, v, *, causal, window_size, kv_cache,
+base_attn_mask, doc_ids)` keeps the reference signature and its results
+(mint/nn/flashattn.py:21-53), with the reference's restrictions lifted:
+
+  - real GQA/MQA (Hq != Hkv) runs on the fused kernel instead of falling back
+    to SDPA (the reference's custom path needs Hq == Hkv, :139);
+  - left sliding windows run on the kernel (the reference sends them to SDPA);
+  - `doc_ids` packing runs as a varlen launch over the document segments of
+    each row (the reference's varlen branch needs flash_attn, :98-137);
+  - the KV-cache path appends on the device at each sequence's own length
+    (no `.item()` sync, :202) and decodes with the split-K kernel.
+
+Extra keyword arguments fuse the positional encoding into the kernels:
+`rope=(cos, sin)` fp32 tables with `start_pos` (q and k are then passed
+UNROTATED), or `alibi_slopes` [Hq]. There is no SDPA or CPU fallback:
+unsupported inputs (an arbitrary `base_attn_mask`, a right window) raise.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from ... import ops
+from ..kvcache.base import KVCache
+
+
+def _segments(doc_ids: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """cu_seqlens of the maximal runs of equal ids inside each row of
+    doc_ids [B, T] (a run never crosses a row). This equals goda's mask
+    doc_ids[i] == doc_ids[j] (mint/nn/flashattn.py:238-240) when every id
+    occupies one contiguous run per row, which is how its packing loader
+    writes them (mint/data/dist/pretrain.py:243-273)."""
+    b, t = doc_ids.shape
+    starts = torch.ones(b, t, dtype=torch.bool, device=doc_ids.device)
+    starts[:, 1:] = doc_ids[:, 1:] != doc_ids[:, :-1]
+    first = starts.reshape(-1).nonzero().reshape(-1).to(torch.int32)
+    cu = torch.cat([first, torch.tensor([b * t], dtype=torch.int32, device=doc_ids.device)])
+    max_len = int((cu[1:] - cu[:-1]).max().item())  # launch size (the reference syncs here too, :121)
+    return cu, max_len
+
+
+class FlashAttention(nn.Module):
+    def __init__(self, *, use_custom_fa: bool = True) -> None:
+        super().__init__()
+        self.use_custom_fa = use_custom_fa  # accepted for signature compatibility
+
+    def forward(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        *,
+        causal: bool = False,
+        window_size: tuple[int, int] = (-1, -1),
+        kv_cache: KVCache | None = None,
+        base_attn_mask: torch.Tensor = None,
+        doc_ids: torch.Tensor = None,
+        rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+        start_pos: int = 0,
+        alibi_slopes: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        if base_attn_mask is not None:
+            raise NotImplementedError(
+                "goda_amd FlashAttention: an arbitrary base_attn_mask is not supported by the HIP kernels "
+                "(causal, left windows, doc_ids packing and ALiBi are)"
+            )
+        if window_size[1] != -1:
+            raise NotImplementedError("goda_amd FlashAttention: only left windows (window_size[1] == -1)")
+        if kv_cache is None:
+            return self._attention(q, k, v, causal=causal, window_left=window_size[0], doc_ids=doc_ids,
+                                   rope=rope, start_pos=start_pos, alibi_slopes=alibi_slopes)
+        if doc_ids is not None:
+            raise NotImplementedError("goda_amd FlashAttention: doc_ids with a KV cache")
+        return self._attention_with_kvcache(q, k, v, kv_cache, causal=causal, window_left=window_size[0],
+                                            rope=rope, alibi_slopes=alibi_slopes)
+
+    # mint/nn/flashattn.py:87-172
+    def _attention(self, q, k, v, *, causal, window_left, doc_ids, rope, start_pos, alibi_slopes):
+        b, t, hq, d = q.shape
+        hkv = k.shape[2]
+        window_left = window_left if window_left >= 0 else -1
+        if doc_ids is not None:
+            if rope is not None:
+                # Positions are row positions, not document positions: rotate
+                # in place on the GPU before packing (RoPE is applied before
+                # attention in goda too, mint/nn/attn.py:60).
+                q, k = _rotate(q, rope, start_pos), _rotate(k, rope, start_pos)
+            cu, max_len = _segments(doc_ids)
+            o = ops.attention_prefill(
+                q.reshape(b * t, hq, d),
+                k.reshape(b * t, hkv, d),
+                v.reshape(b * t, hkv, d),
+                causal=causal,
+                window_left=window_left,
+                alibi_slopes=alibi_slopes,
+                cu_seqlens_q=cu,
+                cu_seqlens_k=cu,
+                max_seqlen_q=max_len,
+                max_seqlen_k=max_len,
+            )
+            return o.reshape(b, t, hq, d)
+        kw = {}
+        if rope is not None:
+            kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True, rope_k=True,
+                      rope_q_offset=start_pos, rope_k_offset=start_pos)
+        return ops.attention_prefill(q, k, v, causal=causal, window_left=window_left,
+                                     alibi_slopes=alibi_slopes, **kw)
+
+    # mint/nn/flashattn.py:174-219
+    def _attention_with_kvcache(self, q, k, v, kv_cache: KVCache, *, causal, window_left, rope, alibi_slopes):
+        b, tq = q.shape[0], q.shape[1]
+        window_left = window_left if window_left >= 0 else -1
+        if rope is not None:
+            kv_cache.append(k, v, rope_cos=rope[0], rope_sin=rope[1])
+        else:
+            kv_cache.append(k, v)
+        k_cache, v_cache, seqlens = kv_cache.get_cache_tensors()
+        used = seqlens[:b]
+        if tq == 1:
+            kw = {}
+            if rope is not None:
+                kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
+            # One new token: the bottom-right causal mask admits every cached
+            # key, so causal and non-causal coincide (mint/nn/flashattn.py:245-264).
+            return ops.attention_decode(q, k_cache, v_cache, used, window_left=window_left,
+                                        alibi_slopes=alibi_slopes, **kw)
+        kw = {}
+        if rope is not None:
+            kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
+        return ops.attention_prefill(q, k_cache[:b], v_cache[:b], causal=causal, window_left=window_left,
+                                     alibi_slopes=alibi_slopes, seqused_k=used, **kw)
+
+
+def _rotate(x: torch.Tensor, rope: tuple[torch.Tensor, torch.Tensor], start_pos: int) -> torch.Tensor:
+    t = x.shape[1]
+    cos = rope[0][start_pos : start_pos + t][None, :, None, :].to(x.dtype)
+    sin = rope[1][start_pos : start_pos + t][None, :, None, :].to(x.dtype)
+    h = x.shape[-1] // 2
+    x1, x2 = x[..., :h], x[..., h:]
+    return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)

@@ -1,0 +1,190 @@
+"""The drop-in layer on the GPU: goda_amd.mint (FlashAttention dispatcher,
+KVCache, attention modules) and goda_amd.kernels_ against the CPU oracle."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from goda_amd import workloads as wl
+from goda_amd.kernels_ import FlashAttentionGQAKernel, FlashAttentionMQAKernel
+from goda_amd.mint.kvcache import KVCache
+from goda_amd.mint.nn import ALiBiPositionalBias, FlashAttention, GroupedQueryAttention, RoPE
+from oracle import attention as ref
+from tests.helpers import TOL, max_err, rope_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(shape, dtype, seed, std=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flashattention_fused_rope_gqa(dtype):
+    b, t, hq, hkv, d = 2, 150, 8, 2, 128
+    q, k, v = _rand((b, t, hq, d), dtype, 1), _rand((b, t, hkv, d), dtype, 2), _rand((b, t, hkv, d), dtype, 3)
+    cos, sin = wl.rope_tables(t + 16, d, 10000.0)
+    fa = FlashAttention()
+    o = fa(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, rope=(cos.to(DEV), sin.to(DEV)), start_pos=5)
+    pos = torch.arange(5, 5 + t)
+    o_ref = ref.attention(rope_oracle(q, cos, sin, pos), rope_oracle(k, cos, sin, pos), v.float(), causal=True)
+    assert max_err(o, o_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("window", [0, 7, 40])
+def test_flashattention_window(window):
+    b, t, hq, hkv, d = 2, 120, 4, 1, 128
+    q, k, v = (_rand((b, t, h, d), torch.bfloat16, 10 + i) for i, h in enumerate((hq, hkv, hkv)))
+    o = FlashAttention()(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, window_size=(window, -1))
+    o_ref = ref.attention(q.float(), k.float(), v.float(), causal=True, window_size=(window, -1))
+    assert max_err(o, o_ref) <= 2e-2
+
+
+@pytest.mark.parametrize("with_rope", [False, True])
+def test_flashattention_doc_ids(with_rope):
+    b, t, hq, hkv, d = 2, 96, 8, 2, 128
+    q, k, v = _rand((b, t, hq, d), torch.bfloat16, 20), _rand((b, t, hkv, d), torch.bfloat16, 21), _rand((b, t, hkv, d), torch.bfloat16, 22)
+    doc = torch.tensor([[0] * 30 + [1] * 50 + [2] * 16, [3] * 96])
+    kw = {}
+    qr, kr = q.float(), k.float()
+    if with_rope:
+        cos, sin = wl.rope_tables(t, d, 10000.0)
+        kw["rope"] = (cos.to(DEV), sin.to(DEV))
+        pos = torch.arange(t)
+        qr, kr = rope_oracle(q, cos, sin, pos), rope_oracle(k, cos, sin, pos)
+    o = FlashAttention()(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, doc_ids=doc.to(DEV), **kw)
+    o_ref = ref.attention(qr, kr, v.float(), causal=True, doc_ids=doc)
+    assert max_err(o, o_ref) <= 2e-2
+
+
+def test_flashattention_refuses_what_it_cannot_run():
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16, device=DEV)
+    fa = FlashAttention()
+    with pytest.raises(NotImplementedError):
+        fa(q, q, q, causal=True, base_attn_mask=torch.ones(1, 1, 8, 8, dtype=torch.bool, device=DEV))
+    with pytest.raises(NotImplementedError):
+        fa(q, q, q, causal=True, window_size=(4, 4))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kvcache_generate_loop_matches_full_causal(dtype):
+    """Prompt through the cache (chunked prefill), then token-by-token decode:
+    every step's output equals the last row of causal attention over the
+    whole sequence so far (the KV-cache invariant), with RoPE fused and the
+    cache holding post-RoPE keys."""
+    b, t0, steps, hq, hkv, d, lmax = 2, 37, 5, 8, 2, 128, 64
+    total = t0 + steps
+    q, k, v = _rand((b, total, hq, d), dtype, 30), _rand((b, total, hkv, d), dtype, 31), _rand((b, total, hkv, d), dtype, 32)
+    cos, sin = wl.rope_tables(lmax, d, 10000.0)
+    rope = (cos.to(DEV), sin.to(DEV))
+    cache = KVCache(max_batch_size=b, max_seq_len=lmax, n_kv_heads=hkv, head_dim=d, dtype=dtype, device=DEV)
+    fa = FlashAttention()
+    outs = [fa(q[:, :t0].to(DEV), k[:, :t0].to(DEV), v[:, :t0].to(DEV), causal=True, kv_cache=cache, rope=rope)]
+    for s in range(t0, total):
+        outs.append(fa(q[:, s : s + 1].to(DEV), k[:, s : s + 1].to(DEV), v[:, s : s + 1].to(DEV), causal=True, kv_cache=cache, rope=rope))
+    torch.cuda.synchronize()
+    assert cache.cache_seqlens.cpu().tolist() == [total] * b
+    o = torch.cat([x.cpu().float() for x in outs], dim=1)
+    pos = torch.arange(total)
+    o_ref = ref.attention(rope_oracle(q, cos, sin, pos), rope_oracle(k, cos, sin, pos), v.float(), causal=True)
+    assert max_err(o, o_ref) <= TOL[dtype]
+    # the cache holds post-RoPE keys and raw values
+    k_ref = rope_oracle(k, cos, sin, pos)
+    assert max_err(cache.k_cache[:, :total], k_ref) <= (1e-5 if dtype == torch.float32 else 1e-2)
+    assert max_err(cache.v_cache[:, :total], v) == 0.0
+
+
+def test_kvcache_update_semantics():
+    """KVCache.update keeps mint/kvcache/base.py:35-50: rows at start_pos for
+    every sequence, lengths = start_pos + T, views up to that row."""
+    b, lmax, hkv, d = 3, 32, 2, 128
+    cache = KVCache(max_batch_size=4, max_seq_len=lmax, n_kv_heads=hkv, head_dim=d, dtype=torch.bfloat16, device=DEV)
+    k1, v1 = _rand((b, 5, hkv, d), torch.bfloat16, 40), _rand((b, 5, hkv, d), torch.bfloat16, 41)
+    kf, vf = cache.update(k1.to(DEV), v1.to(DEV), start_pos=3)
+    assert kf.shape == (b, 8, hkv, d)
+    assert torch.equal(kf[:, 3:].cpu(), k1) and torch.equal(vf[:, 3:].cpu(), v1)
+    assert cache.cache_seqlens.cpu().tolist() == [8, 8, 8, 0]
+    k, vv = cache.get()
+    assert k.shape[1] == 8
+    cache.reset()
+    assert cache.cache_seqlens.cpu().tolist() == [0, 0, 0, 0]
+    cache.clear()
+    assert torch.count_nonzero(cache.k_cache).item() == 0
+
+
+def _layer_reference(layer: GroupedQueryAttention, x: torch.Tensor, rope: RoPE | None, slopes=None):
+    """goda's GroupedQueryAttention.forward (mint/nn/attn.py:39-77) in fp32 on
+    the CPU with the oracle's attention."""
+    sd = {n: p.detach().cpu().float() for n, p in layer.named_parameters()}
+    xb = x.cpu().float()
+    bsz, t, _ = xb.shape
+
+    def rms(y, scale):
+        return y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + scale)
+
+    q = (xb @ sd["wq.weight"].T).view(bsz, t, layer.n_heads, layer.head_dim)
+    k = (xb @ sd["wk.weight"].T).view(bsz, t, layer.n_kv_heads, layer.head_dim)
+    v = (xb @ sd["wv.weight"].T).view(bsz, t, layer.n_kv_heads, layer.head_dim)
+    q, k = rms(q, sd["q_norm.scale"]), rms(k, sd["k_norm.scale"])
+    if rope is not None:
+        pos = torch.arange(t)
+        q = ref.apply_rope(q, rope.cos.cpu(), rope.sin.cpu(), pos)
+        k = ref.apply_rope(k, rope.cos.cpu(), rope.sin.cpu(), pos)
+    w = (layer.window_size, -1) if layer.window_size > 0 else (-1, -1)
+    o = ref.attention(q, k, v, causal=True, window_size=w, alibi_slopes=slopes)
+    return o.reshape(bsz, t, -1) @ sd["wo.weight"].T
+
+
+@pytest.mark.parametrize("window", [-1, 24])
+def test_gqa_layer_with_fused_rope(window):
+    torch.manual_seed(0)
+    e, hq, hkv, d, t = 256, 4, 2, 128, 64
+    rope = RoPE(seq_len=128, head_dim=d, rope_base_theta=10000)
+    layer = GroupedQueryAttention(hq, hkv, d, e, rope, torch.float32, window_size=window)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.05)
+    x = torch.randn(2, t, e) * 0.5
+    layer = layer.to(DEV)
+    with torch.no_grad():
+        y = layer(x.to(DEV))
+    y_ref = _layer_reference(layer, x, rope)
+    assert max_err(y, y_ref) <= 1e-4 * max(1.0, y_ref.abs().max().item())
+
+
+def test_gqa_layer_with_alibi():
+    torch.manual_seed(1)
+    e, hq, hkv, d, t = 256, 8, 1, 128, 48
+    layer = GroupedQueryAttention(hq, hkv, d, e, ALiBiPositionalBias(hq), torch.float32)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.05)
+    x = torch.randn(1, t, e) * 0.5
+    layer = layer.to(DEV)
+    with torch.no_grad():
+        y = layer(x.to(DEV))
+    slopes = torch.tensor(ref.alibi_slopes(hq), dtype=torch.float32)
+    y_ref = _layer_reference(layer, x, None, slopes)
+    assert max_err(y, y_ref) <= 1e-4 * max(1.0, y_ref.abs().max().item())
+
+
+@pytest.mark.parametrize("cls", [FlashAttentionGQAKernel, FlashAttentionMQAKernel])
+@pytest.mark.parametrize("hkv", [8, 2, 1])
+def test_kernels_apply_signature(cls, hkv):
+    """kernels_/flash_attn_gqa/cuda.py:515-575: apply(Q, K, V, causal, tau) on
+    [B, H, T, D], here also with Hkv < Hq heads in K and V."""
+    b, hq, t, d = 2, 8, 100, 128
+    q = _rand((b, hq, t, d), torch.bfloat16, 50)
+    k = _rand((b, hkv, t, d), torch.bfloat16, 51)
+    v = _rand((b, hkv, t, d), torch.bfloat16, 52)
+    tau = 1.0 / math.sqrt(d)
+    with torch.no_grad():
+        o = cls.apply(q.to(DEV), k.to(DEV), v.to(DEV), True, tau)
+    assert o.shape == (b, hq, t, d)
+    o_ref = ref.attention(q.transpose(1, 2).float(), k.transpose(1, 2).float(), v.transpose(1, 2).float(), causal=True)
+    assert max_err(o.transpose(1, 2), o_ref) <= 2e-2

@@ -1,0 +1,78 @@
+"""CPU tests of the host-side logic of the drop-in layer and the workload
+definitions (no GPU work)."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from goda_amd import workloads as wl
+from goda_amd.mint.nn import FlashAttention, LinearScaledRoPE, RoPE, alibi_slopes
+from goda_amd.mint.nn.flashattn import _segments
+from oracle import attention as ref
+
+
+def test_alibi_slopes_match_oracle():
+    for n in (1, 2, 3, 6, 8, 12, 16, 32):
+        assert alibi_slopes(n) == ref.alibi_slopes(n) == wl.alibi_slopes(n)
+
+
+def test_rope_tables_match_oracle():
+    r = RoPE(seq_len=300, head_dim=128, rope_base_theta=10000)
+    cos, sin = ref.rope_tables(300, 128, 10000.0)
+    assert torch.equal(r.cos, cos) and torch.equal(r.sin, sin)
+    c2, s2 = wl.rope_tables(300, 128, 10000.0)
+    assert torch.equal(c2, cos) and torch.equal(s2, sin)
+    rl = LinearScaledRoPE(seq_len=64, head_dim=64, scale_factor=4.0, rope_base_theta=10000)
+    cl, sl = ref.rope_tables(64, 64, 10000.0, scale_factor=4.0)
+    assert torch.equal(rl.cos, cl) and torch.equal(rl.sin, sl)
+
+
+def test_rope_forward_matches_oracle():
+    r = RoPE(seq_len=64, head_dim=32, rope_base_theta=10000)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 10, 3, 32, generator=g)
+    k = torch.randn(2, 10, 1, 32, generator=g)
+    q2, k2, bias = r(q, k, start_pos=7)
+    pos = torch.arange(7, 17)
+    assert bias is None
+    assert torch.allclose(q2, ref.apply_rope(q, r.cos, r.sin, pos), atol=1e-6)
+    assert torch.allclose(k2, ref.apply_rope(k, r.cos, r.sin, pos), atol=1e-6)
+
+
+def test_segments_match_oracle():
+    doc = torch.tensor([[0, 0, 1, 1, 1, 2], [7, 7, 7, 7, 8, 8], [3, 3, 3, 3, 3, 3]])
+    cu, mx = _segments(doc)
+    assert cu.tolist() == ref.doc_ids_to_cu_seqlens(doc).tolist() == [0, 2, 5, 6, 10, 12, 18]
+    assert mx == 6
+
+
+def test_flop_and_byte_counts_closed_form():
+    w = wl.CFG2
+    assert wl.prefill_flops(w) == 4 * 128 * 32 * 4 * 8192 * 8193 / 2
+    lens = torch.tensor([1024, 2048], dtype=torch.int32)
+    w4 = wl.Decode("t", torch.bfloat16, 2, 32, 8, 128, 4096, (1, 1))
+    assert wl.decode_bytes(w4, lens) == (1024 + 2048) * 8 * 128 * 2 * 2 + 2 * 32 * 128 * 2 * 2
+    nc = wl.Prefill("nc", torch.bfloat16, 2, 10, 4, 1, 64, causal=False)
+    assert wl.prefill_flops(nc) == 4 * 64 * 4 * 2 * 100
+
+
+def test_workload_seeds_are_deterministic():
+    a = wl.prefill_inputs(wl.Prefill("t", torch.bfloat16, 1, 16, 2, 1, 64, seed=3), "cpu")
+    b = wl.prefill_inputs(wl.Prefill("t", torch.bfloat16, 1, 16, 2, 1, 64, seed=3), "cpu")
+    assert torch.equal(a["q"], b["q"]) and torch.equal(a["v"], b["v"])
+    lens = wl.seq_lengths(1024, 32768, 64, 405)
+    assert lens.min() >= 1024 and lens.max() <= 32768 and lens.dtype == torch.int32
+
+
+def test_flashattention_refuses_cpu_and_unsupported_masks():
+    fa = FlashAttention()
+    q = torch.zeros(1, 4, 2, 64)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        fa(q, q, q, causal=True)
+    with pytest.raises(NotImplementedError):
+        fa(q, q, q, causal=True, base_attn_mask=torch.ones(1, 1, 4, 4, dtype=torch.bool))
+    with pytest.raises(NotImplementedError):
+        fa(q, q, q, causal=True, window_size=(2, 2))
