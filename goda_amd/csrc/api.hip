@@ -128,8 +128,10 @@ int32_t goda_attn_prefill_fwd(const goda_prefill_args* a, void* stream) {
 int64_t goda_attn_decode_workspace_size(const goda_decode_args* a) {
   if (!a) return fail(GODA_ERR_INVALID_ARG, "decode: args is NULL");
   if (!goda::decode_mfma_supported(*a)) return 0;
-  const int split = a->split_size > 0 ? a->split_size : goda::decode_default_split(*a);
-  return goda::decode_workspace_bytes(*a, split);
+  if (a->heads_q <= 0 || a->heads_kv <= 0 || a->heads_q % a->heads_kv != 0)
+    return fail(GODA_ERR_INVALID_ARG, "decode: heads_q %d must be a positive multiple of heads_kv %d",
+                a->heads_q, a->heads_kv);
+  return goda::decode_workspace_bytes(*a);
 }
 
 int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
@@ -165,9 +167,9 @@ int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
     p.a = *a;
     p.group = a->heads_q / a->heads_kv;
     p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
-    p.split = a->split_size > 0 ? a->split_size : goda::decode_default_split(*a);
-    p.nsplit_max = a->max_seqlen > 0 ? (a->max_seqlen + p.split - 1) / p.split : 1;
-    const int64_t need = goda::decode_workspace_bytes(*a, p.split);
+    p.split = a->split_size;
+    p.nslots = goda::decode_slots(*a);
+    const int64_t need = goda::decode_workspace_bytes(*a);
     if (need > 0 && (!a->workspace || a->workspace_bytes < need))
       return fail(GODA_ERR_WORKSPACE, "decode: workspace of %lld bytes needed, %lld given",
                   (long long)need, (long long)a->workspace_bytes);

@@ -1,10 +1,21 @@
-// One-token decode attention over a contiguous KV cache (bf16 / fp16),
-// split-K over the cached keys with a log-sum-exp merge, plus the KV append.
+// One-token decode attention over a contiguous KV cache (bf16 / fp16) with
+// per-sequence lengths, plus the KV append.
 //
-// decode_splitk_kernel: one workgroup per (split, KV head x head slice,
-// sequence). The split covers `split` consecutive keys of the sequence's valid
-// range; the workgroup's 4 waves take 16-key chunks of it in turn, each with
-// its own online-softmax state, and merge through LDS at the end.
+// Work decomposition (balanced split-K). The visible keys of every unit
+// (sequence b, KV head, slice of that head's query heads) are laid end to end,
+// sequence-major, in one flattened key space of `total` keys. The space is cut
+// into ranges of `per` keys that a persistent grid of workgroups (as many as
+// the GPU holds at once) takes in turn. With the default per = total / grid
+// every workgroup reads the same number of cache bytes whatever the mix of
+// lengths, and nothing is launched for keys that do not exist. A range covers
+// pieces (segments) of one or more units:
+//   - a segment that is a whole unit writes o and lse directly;
+//   - a partial segment writes (o normalised, lse) to one of the range's two
+//     workspace slots (slot 0: its first segment, slot 1: its last), and
+//     merge_kernel combines a unit's partials:
+//       lse = log sum_s exp(lse_s), o = sum_s exp(lse_s - lse) o_s.
+// Inside a segment the workgroup's 4 waves take 16-key chunks in turn, each
+// with its own online-softmax state, and merge through LDS at the end:
 //   scores  S^T[16 keys][16 heads] = K[16 keys][D] . Q^T[D][heads]
 //           on 16x16x32 MFMA; K rows are loaded straight from the cache into
 //           the A operand (16 bytes per lane), Q^T lives in VGPRs. All query
@@ -12,9 +23,10 @@
 //   values  O[head][d] += p[head][key] * V[key][d] on the vector ALUs: each
 //           lane owns 8 consecutive head-dim elements (16-byte loads, a wave
 //           instruction reads whole cache rows), p is broadcast through LDS.
-// A sequence whose keys fit in one split is written directly; otherwise each
-// split writes (o_s normalised, lse_s) to the workspace and merge_kernel
-// combines them: lse = log sum_s exp(lse_s), o = sum_s exp(lse_s - lse) o_s.
+
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "common.h"
 #include "launch.h"
@@ -23,7 +35,20 @@ namespace goda {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kChunk = 16;  // keys per wave step
+constexpr int kChunk = 16;              // keys per wave step
+constexpr float kRescaleThresh = 8.0f;  // log2 units
+constexpr int NBUF = 2;                 // 16-key chunks in flight per wave
+constexpr int kMinRange = 64;           // keys; ranges are multiples of this
+constexpr int kMaxGrid = 2048;          // persistent grid bound (sizes the workspace)
+
+// Max over the four lanes l16, l16+16, l16+32, l16+48 (the key groups of one
+// head): permlane16/32 swaps exchange the halves without an LDS round trip.
+__device__ __forceinline__ float group_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 template <typename T>
 struct V8;
@@ -36,68 +61,148 @@ struct V8<f16> {
   typedef f16x8 t;
 };
 
-// Valid key range [kbeg, kend) of sequence b and its split count.
-struct KeyRange {
-  int kbeg, kend, nsplit;
-};
-__device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int b) {
-  const goda_decode_args& a = p.a;
-  int L = a.cache_seqlens[b];
-  L = max(0, min(L, a.max_seqlen));
-  KeyRange r;
-  r.kend = L;
-  r.kbeg = (a.window_left >= 0) ? max(0, L - 1 - a.window_left) : 0;
-  const int n = r.kend - r.kbeg;
-  r.nsplit = n > 0 ? (n + p.split - 1) / p.split : 0;
-  return r;
+// Wave-uniform copies (scalar registers) of values every lane holds equally.
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ long long uniform(long long x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((unsigned long long)x >> 32));
+  return (long long)(((unsigned long long)hi << 32) | lo);
 }
 
+// Visible keys of sequence b: [kbeg, kbeg + n) with kbeg + n = its length.
+__device__ __forceinline__ int visible(const goda_decode_args& a, int b, int* kbeg) {
+  int L = a.cache_seqlens[b];
+  L = max(0, min(L, a.max_seqlen));
+  const int k0 = (a.window_left >= 0) ? max(0, L - 1 - a.window_left) : 0;
+  *kbeg = k0;
+  return L - k0;
+}
+
+// Keys per range: the caller's split, else total / grid rounded up.
+__device__ __forceinline__ int64_t range_keys(int64_t total, int grid, int split) {
+  if (split > 0) return split;
+  const int64_t q = (total + grid - 1) / grid;
+  return max((int64_t)kMinRange, (q + kMinRange - 1) / kMinRange * kMinRange);
+}
+
+// Wave-wide sums of the visible key counts: over all sequences, and over the
+// sequences before `b` (every lane returns both).
+__device__ __forceinline__ void visible_sums(const goda_decode_args& a, int b, long long* all,
+                                             long long* before) {
+  const int lane = threadIdx.x & 63;
+  long long s = 0, sb = 0;
+  for (int i = lane; i < a.batch; i += 64) {
+    int k0;
+    const int n = visible(a, i, &k0);
+    s += n;
+    if (i < b) sb += n;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    s += __shfl_xor(s, o, 64);
+    sb += __shfl_xor(sb, o, 64);
+  }
+  *all = uniform(s);
+  *before = uniform(sb);
+}
+
+// Position in the flattened key space: sequence b whose block of U * n keys
+// starts at `base` and holds the position.
+struct Cursor {
+  int b, kbeg, n;
+  int64_t base;
+};
+
+// The sequence holding flattened position R (R < total), by a wave-wide
+// inclusive scan of U * n over 64 sequences at a time.
+__device__ Cursor locate(const goda_decode_args& a, int U, int64_t R) {
+  const int lane = threadIdx.x & 63;
+  long long base = 0;
+  Cursor c{0, 0, 0, 0};
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    int k0 = 0;
+    const long long n = b < a.batch ? (long long)U * visible(a, b, &k0) : 0;
+    long long incl = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const long long t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(base + incl > R);
+    if (hit != 0) {
+      const int l = __builtin_ctzll(hit);
+      c.b = b0 + l;
+      c.base = base + uniform(__shfl(incl - n, l, 64));
+      c.n = uniform(__shfl((int)(n / U), l, 64));
+      c.kbeg = uniform(__shfl(k0, l, 64));
+      return c;
+    }
+    base += uniform(__shfl(incl, 63, 64));
+  }
+  return c;  // not reached for R < total
+}
+
+// Moves the cursor to the next sequence with visible keys; false if none.
+__device__ __forceinline__ bool advance(const goda_decode_args& a, int U, Cursor& c) {
+  c.base += (int64_t)U * c.n;
+  while (c.b + 1 < a.batch) {
+    ++c.b;
+    c.n = visible(a, c.b, &c.kbeg);
+    if (c.n > 0) return true;
+  }
+  return false;
+}
+
+struct Segment {
+  int b, hk, hs;   // sequence, KV head, slice of its query heads
+  int sbeg, send;  // absolute key positions [sbeg, send)
+  int qpos;        // absolute position of the query token
+  bool whole;      // the segment is the whole unit: write o directly
+  int64_t slot;    // workspace slot of a partial segment
+};
+
+template <int D, int HMAX>
+struct DecodeSmem {
+  float p[kWaves][kChunk][16];
+  float alpha[kWaves][16];
+  float m[kWaves][HMAX];
+  float l[kWaves][HMAX];
+  float o[kWaves][HMAX][D];
+};
+
+// Attention of the segment's query heads over its keys; ends with a
+// workgroup barrier so the LDS can be reused by the next segment.
 template <typename T, int D, int HMAX>
-__global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const DecodeParams p) {
+__device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segment& sg) {
+  // The launch parameters are re-read from the kernel argument segment for
+  // every segment (scalar loads) rather than held in scalar registers across
+  // the segment loop, which would spill them.
+  typedef __attribute__((address_space(4))) const DecodeParams* ParamsPtr;
+  ParamsPtr pp = (ParamsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pp));
+  const DecodeParams& p = *pp;
   typedef typename V8<T>::t v8;
   constexpr int KS = D / 32;    // k-steps of the 16x16x32 score MFMA
   constexpr int CPL = D / 128;  // 8-element head-dim chunks per lane in PV
   static_assert(CPL >= 1, "head_dim >= 128");
   const goda_decode_args& a = p.a;
 
-  __shared__ float p_lds[kWaves][kChunk][16];
-  __shared__ float alpha_lds[kWaves][16];
-  __shared__ float red_m[kWaves][HMAX];
-  __shared__ float red_l[kWaves][HMAX];
-  __shared__ float red_o[kWaves][HMAX][D];
-
-  const int s = blockIdx.x;
-  const int nhs = (p.group + HMAX - 1) / HMAX;
-  const int hk = blockIdx.y / nhs;
-  const int hs = blockIdx.y % nhs;
-  const int b = blockIdx.z;
-  const int hq0 = hk * p.group + hs * HMAX;
-  const int nh = min(HMAX, p.group - hs * HMAX);
-
-  const KeyRange kr = key_range(p, b);
-  const int tid = threadIdx.x;
-  T* obase = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_stride_b;
-  if (kr.nsplit == 0) {
-    // No visible key: o = 0, lse = -inf (written once, by split 0).
-    if (s == 0) {
-      for (int idx = tid; idx < nh * D; idx += kWaves * 64) {
-        const int h = idx / D, d = idx % D;
-        obase[(int64_t)(hq0 + h) * a.o_stride_h + d] = (T)0.f;
-      }
-      if (a.lse && tid < nh) a.lse[(int64_t)b * a.lse_stride_b + hq0 + tid] = kNegInf;
-    }
-    return;
-  }
-  if (s >= kr.nsplit) return;
-  const int sbeg = kr.kbeg + s * p.split;
-  const int send = min(kr.kend, sbeg + p.split);
-
+  const int b = sg.b;
+  const int hq0 = sg.hk * p.group + sg.hs * HMAX;
+  const int nh = min(HMAX, p.group - sg.hs * HMAX);
+  const int sbeg = sg.sbeg, send = sg.send;
+  // The lane index is made opaque per segment: otherwise the compiler hoists
+  // every lane-dependent address product out of the segment loop and keeps
+  // them all live through the chunk loop.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int kg = lane >> 4;  // 4 lane groups of 16
   const bool head_ok = l16 < nh;
-  const int qpos = kr.kend - 1;  // absolute position of the query token
+  const int qpos = sg.qpos;
 
   // Q^T operand: lane -> head l16, head-dim 32*ks + 8*kg + e.
   v8 qf[KS];
@@ -127,9 +232,9 @@ __global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const Decode
   const float slope2 = (alibi && head_ok) ? a.alibi_slopes[hq0 + l16] * kLog2e : 0.f;
 
   const T* kbase = reinterpret_cast<const T*>(a.k_cache) + (int64_t)b * a.k_stride_b +
-                   (int64_t)hk * a.k_stride_h;
+                   (int64_t)sg.hk * a.k_stride_h;
   const T* vbase = reinterpret_cast<const T*>(a.v_cache) + (int64_t)b * a.v_stride_b +
-                   (int64_t)hk * a.v_stride_h;
+                   (int64_t)sg.hk * a.v_stride_h;
 
   float acc[HMAX][CPL][8];
 #pragma unroll
@@ -140,29 +245,27 @@ __global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const Decode
       for (int e = 0; e < 8; ++e) acc[h][i][e] = 0.f;
   float m_run = kNegInf, l_run = 0.f;  // for head l16 over this lane's keys
 
+  // Each wave takes chunks wave, wave+4, ... of 16 keys.
   const int nchunks = (send - sbeg + kChunk - 1) / kChunk;
-  for (int ch = wave; ch < nchunks; ch += kWaves) {
+  auto load = [&](int ch, v8 (&kf)[KS], v8 (&vf)[4][CPL]) {
     const int k0 = sbeg + ch * kChunk;
-    // K operand rows (clamped inside the sequence; masked below).
-    const int krow = min(k0 + l16, send - 1);
-    v8 kf[KS];
-    const T* kp = kbase + (int64_t)krow * a.k_stride_t;
+    // K operand rows (clamped inside the segment; masked in the softmax).
+    const T* kp = kbase + (int64_t)min(k0 + l16, send - 1) * a.k_stride_t;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = ld_vec<v8>(kp + 32 * ks + 8 * kg);
     // V rows for the PV step: keys k0 + 4*kg + kk, head-dim chunk l16 (+16 i).
-    v8 vf[4][CPL];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const int vrow = min(k0 + 4 * kg + kk, send - 1);
-      const T* vp = vbase + (int64_t)vrow * a.v_stride_t;
+      const T* vp = vbase + (int64_t)min(k0 + 4 * kg + kk, send - 1) * a.v_stride_t;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) vf[kk][i] = ld_vec<v8>(vp + 8 * (l16 + 16 * i));
     }
-
+  };
+  auto process = [&](int ch, const v8 (&kf)[KS], const v8 (&vf)[4][CPL]) {
+    const int k0 = sbeg + ch * kChunk;
     f32x4 sc = f32x4{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) sc = mfma16(kf[ks], qf[ks], sc);
-
     // sc[r]: head l16, key k0 + 4*kg + r.
     float t[4];
     float mx = kNegInf;
@@ -174,36 +277,40 @@ __global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const Decode
       t[r] = (key < send) ? x : kNegInf;
       mx = fmaxf(mx, t[r]);
     }
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
-    float lsum = 0.f;
+    mx = group_max(mx);
+    // Lazy rescale: the reference max of a head only moves when the chunk
+    // max exceeds it by more than kRescaleThresh (log2 units).
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleThresh) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      if (kg == 0) sm.alpha[wave][l16] = alpha;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int h4 = 0; h4 < HMAX / 4; ++h4) {
+        const f32x4 al = ld_vec<f32x4>(&sm.alpha[wave][4 * h4]);
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+          for (int i = 0; i < CPL; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[4 * h4 + hh][i][e] *= al[hh];
+      }
+    }
+    const float m_use = (m_run == kNegInf) ? 0.f : m_run;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float pr = fast_exp2(t[r] - m_use);
-      lsum += pr;
-      p_lds[wave][4 * kg + r][l16] = pr;
+      l_run += pr;
+      sm.p[wave][4 * kg + r][l16] = pr;
     }
-    l_run = l_run * alpha + lsum;
-    if (kg == 0) alpha_lds[wave][l16] = alpha;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // Rescale and accumulate this lane's 4 keys for every head of the slice.
-#pragma unroll
-    for (int h4 = 0; h4 < HMAX / 4; ++h4) {
-      const f32x4 al = ld_vec<f32x4>(&alpha_lds[wave][4 * h4]);
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh)
-#pragma unroll
-        for (int i = 0; i < CPL; ++i)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[4 * h4 + hh][i][e] *= al[hh];
-    }
+    // Accumulate this lane's 4 keys for every head of the slice.
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       float vv[CPL][8];
@@ -213,7 +320,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const Decode
         for (int e = 0; e < 8; ++e) vv[i][e] = (float)vf[kk][i][e];
 #pragma unroll
       for (int h4 = 0; h4 < HMAX / 4; ++h4) {
-        const f32x4 pv = ld_vec<f32x4>(&p_lds[wave][4 * kg + kk][4 * h4]);
+        const f32x4 pv = ld_vec<f32x4>(&sm.p[wave][4 * kg + kk][4 * h4]);
 #pragma unroll
         for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
@@ -226,6 +333,24 @@ __global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const Decode
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // Ring of NBUF register sets: chunk ch + (NBUF-1)*kWaves is in flight while
+  // chunk ch is processed (the unrolled loop keeps every buffer index static).
+  v8 kb[NBUF][KS], vb[NBUF][4][CPL];
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i)
+    if (wave + i * kWaves < nchunks) load(wave + i * kWaves, kb[i], vb[i]);
+  for (int base = wave; base < nchunks; base += NBUF * kWaves) {
+#pragma unroll
+    for (int u = 0; u < NBUF; ++u) {
+      const int ch = base + u * kWaves;
+      if (ch < nchunks) {
+        const int nxt = ch + (NBUF - 1) * kWaves;
+        if (nxt < nchunks) load(nxt, kb[(u + NBUF - 1) % NBUF], vb[(u + NBUF - 1) % NBUF]);
+        process(ch, kb[u], vb[u]);
+      }
+    }
   }
 
   // ---- reduce within the wave -------------------------------------------------
@@ -244,94 +369,207 @@ __global__ void __launch_bounds__(kWaves * 64) decode_splitk_kernel(const Decode
       }
   if (kg == 0) {
     if (l16 < HMAX) {
-      red_m[wave][l16] = m_run;
-      red_l[wave][l16] = l_run;
+      sm.m[wave][l16] = m_run;
+      sm.l[wave][l16] = l_run;
     }
 #pragma unroll
     for (int h = 0; h < HMAX; ++h)
 #pragma unroll
       for (int i = 0; i < CPL; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) red_o[wave][h][8 * (l16 + 16 * i) + e] = acc[h][i][e];
+        for (int e = 0; e < 8; ++e) sm.o[wave][h][8 * (l16 + 16 * i) + e] = acc[h][i][e];
   }
   __syncthreads();
 
-  // ---- merge the waves, write output or split partial --------------------------
-  const bool single = kr.nsplit == 1;
+  // ---- merge the waves, write the output or the partial ----------------------
+  T* obase = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_stride_b;
   float* part_o = reinterpret_cast<float*>(a.workspace);
-  float* part_lse = part_o + (int64_t)a.batch * a.heads_q * p.nsplit_max * D;
+  float* part_lse = part_o + p.nslots * HMAX * D;
   for (int idx = tid; idx < nh * D; idx += kWaves * 64) {
     const int h = idx / D, d = idx % D;
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_m[w][h]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm.m[w][h]);
     const float Mu = (M == kNegInf) ? 0.f : M;
     float lsum = 0.f, o = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(red_m[w][h] - Mu);
-      lsum = fmaf(f, red_l[w][h], lsum);
-      o = fmaf(f, red_o[w][h][d], o);
+      const float f = fast_exp2(sm.m[w][h] - Mu);
+      lsum = fmaf(f, sm.l[w][h], lsum);
+      o = fmaf(f, sm.o[w][h][d], o);
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const float lse = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : kNegInf;
     const int hq = hq0 + h;
-    if (single) {
+    if (sg.whole) {
       obase[(int64_t)hq * a.o_stride_h + d] = (T)(o * inv);
       if (a.lse && d == 0) a.lse[(int64_t)b * a.lse_stride_b + hq] = lse;
     } else {
-      const int64_t slot = ((int64_t)b * a.heads_q + hq) * p.nsplit_max + s;
-      part_o[slot * D + d] = o * inv;
-      if (d == 0) part_lse[slot] = lse;
+      part_o[(sg.slot * HMAX + h) * D + d] = o * inv;
+      if (d == 0) part_lse[sg.slot * HMAX + h] = lse;
+    }
+  }
+  __syncthreads();
+}
+
+// Waves per SIMD the register allocation must allow (1: no constraint).
+template <int D, int HMAX>
+constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : 1;
+
+// The kernel's only argument sits at offset 0 of the kernel argument segment
+// (run_segment reads it from there).
+template <typename T, int D, int HMAX>
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<D, HMAX>)))
+decode_splitk_kernel(const DecodeParams p) {
+  __shared__ DecodeSmem<D, HMAX> sm;
+  const goda_decode_args& a = p.a;
+  const int nhs = (p.group + HMAX - 1) / HMAX;
+  const int U = a.heads_kv * nhs;
+  long long all, unused;
+  visible_sums(a, 0, &all, &unused);
+  const int64_t total = (int64_t)U * all;
+  const int64_t per = range_keys(total, gridDim.x, p.split);
+  const int64_t nranges = (total + per - 1) / per;
+
+  for (int64_t r = blockIdx.x; r < nranges; r += gridDim.x) {
+    const int64_t R0 = r * per;
+    const int64_t R1 = min(total, R0 + per);
+    Cursor cur = locate(a, U, R0);
+    int64_t pos = R0;
+    bool first = true;
+    while (pos < R1) {
+      if (pos >= cur.base + (int64_t)U * cur.n && !advance(a, U, cur)) return;
+      const int64_t in_b = pos - cur.base;
+      const int j = uniform((int)(in_b / cur.n));
+      const int off = uniform((int)(in_b - (int64_t)j * cur.n));
+      const int len = (int)min((int64_t)(cur.n - off), R1 - pos);
+      Segment sg;
+      sg.b = cur.b;
+      sg.hk = j / nhs;
+      sg.hs = j % nhs;
+      sg.sbeg = cur.kbeg + off;
+      sg.send = sg.sbeg + len;
+      sg.qpos = cur.kbeg + cur.n - 1;
+      sg.whole = (off == 0 && len == cur.n);
+      sg.slot = 2 * r + (first ? 0 : 1);
+      run_segment<T, D, HMAX>(sm, sg);
+      pos += len;
+      first = false;
     }
   }
 }
 
-template <typename T, int D>
-__global__ void __launch_bounds__(D) merge_kernel(const DecodeParams p) {
+// One workgroup per (unit, sequence): combines the partials of a unit that
+// spans several ranges, and writes o = 0, lse = -inf for a sequence with no
+// visible key. Units held whole by one range were written by the main kernel.
+template <typename T, int D, int HMAX>
+__global__ void __launch_bounds__(256) merge_kernel(const DecodeParams p) {
   const goda_decode_args& a = p.a;
-  const int hq = blockIdx.x;
+  const int nhs = (p.group + HMAX - 1) / HMAX;
+  const int U = a.heads_kv * nhs;
+  const int j = blockIdx.x;
   const int b = blockIdx.y;
-  const KeyRange kr = key_range(p, b);
-  if (kr.nsplit <= 1) return;
-  const int d = threadIdx.x;
-  const float* part_o = reinterpret_cast<const float*>(a.workspace);
-  const float* part_lse = part_o + (int64_t)a.batch * a.heads_q * p.nsplit_max * D;
-  const int64_t slot0 = ((int64_t)b * a.heads_q + hq) * p.nsplit_max;
-  float M = kNegInf;
-  for (int s = 0; s < kr.nsplit; ++s) M = fmaxf(M, part_lse[slot0 + s]);
-  const float Mu = (M == kNegInf) ? 0.f : M;
-  float wsum = 0.f, o = 0.f;
-  for (int s = 0; s < kr.nsplit; ++s) {
-    const float w = __expf(part_lse[slot0 + s] - Mu);
-    wsum += w;
-    o = fmaf(w, part_o[(slot0 + s) * D + d], o);
+  const int hk = j / nhs, hs = j % nhs;
+  const int hq0 = hk * p.group + hs * HMAX;
+  const int nh = min(HMAX, p.group - hs * HMAX);
+  long long all, before;
+  visible_sums(a, b, &all, &before);
+  int kbeg;
+  const int n = visible(a, b, &kbeg);
+  T* obase = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_stride_b;
+  if (n == 0) {
+    for (int idx = threadIdx.x; idx < nh * D; idx += 256) {
+      const int h = idx / D, d = idx % D;
+      obase[(int64_t)(hq0 + h) * a.o_stride_h + d] = (T)0.f;
+      if (a.lse && d == 0) a.lse[(int64_t)b * a.lse_stride_b + hq0 + h] = kNegInf;
+    }
+    return;
   }
-  T* out = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h;
-  out[d] = (T)(wsum > 0.f ? o / wsum : 0.f);
-  if (a.lse && d == 0) a.lse[(int64_t)b * a.lse_stride_b + hq] = wsum > 0.f ? Mu + logf(wsum) : kNegInf;
+  const int64_t total = (int64_t)U * all;
+  const int64_t per = range_keys(total, p.grid, p.split);
+  const int64_t S = (int64_t)U * before + (int64_t)j * n;
+  const int64_t r0 = S / per, r1 = (S + n - 1) / per;
+  if (r0 == r1) return;  // written whole by the range that holds it
+  const float* part_o = reinterpret_cast<const float*>(a.workspace);
+  const float* part_lse = part_o + p.nslots * HMAX * D;
+  // The unit is the last segment of range r0 (slot 1) unless it starts that
+  // range (slot 0), and the first segment (slot 0) of every later range.
+  const int64_t slot0 = 2 * r0 + (S == r0 * per ? 0 : 1);
+  for (int idx = threadIdx.x; idx < nh * D; idx += 256) {
+    const int h = idx / D, d = idx % D;
+    float M = kNegInf;
+    for (int64_t r = r0; r <= r1; ++r) {
+      const int64_t sl = r == r0 ? slot0 : 2 * r;
+      M = fmaxf(M, part_lse[sl * HMAX + h]);
+    }
+    const float Mu = (M == kNegInf) ? 0.f : M;
+    float wsum = 0.f, o = 0.f;
+    for (int64_t r = r0; r <= r1; ++r) {
+      const int64_t sl = r == r0 ? slot0 : 2 * r;
+      const float w = __expf(part_lse[sl * HMAX + h] - Mu);
+      wsum += w;
+      o = fmaf(w, part_o[(sl * HMAX + h) * D + d], o);
+    }
+    const int hq = hq0 + h;
+    obase[(int64_t)hq * a.o_stride_h + d] = (T)(wsum > 0.f ? o / wsum : 0.f);
+    if (a.lse && d == 0) a.lse[(int64_t)b * a.lse_stride_b + hq] = wsum > 0.f ? Mu + logf(wsum) : kNegInf;
+  }
+}
+
+// Workgroups of `kernel` the device holds at once (cached per device).
+hipError_t persistent_grid(const void* kernel, int* grid) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({kernel, dev});
+  if (it != cache.end()) {
+    *grid = it->second;
+    return hipSuccess;
+  }
+  int cus = 0, occ = 0;
+  if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+  if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kWaves * 64, 0)) != hipSuccess) return e;
+  const int g = max(1, min(kMaxGrid, cus * max(1, occ)));
+  cache[{kernel, dev}] = g;
+  *grid = g;
+  return hipSuccess;
 }
 
 template <typename T, int D, int HMAX>
-hipError_t launch_hd(const DecodeParams& p, hipStream_t s) {
+hipError_t launch_hd(DecodeParams p, hipStream_t s) {
   const goda_decode_args& a = p.a;
-  const int nhs = (p.group + HMAX - 1) / HMAX;
-  dim3 grid(p.nsplit_max, a.heads_kv * nhs, a.batch);
-  hipError_t e = record_timing(a.timing_begin, s);
+  hipError_t e =
+      persistent_grid(reinterpret_cast<const void*>(&decode_splitk_kernel<T, D, HMAX>), &p.grid);
   if (e != hipSuccess) return e;
-  decode_splitk_kernel<T, D, HMAX><<<grid, kWaves * 64, 0, s>>>(p);
+  if ((e = record_timing(a.timing_begin, s)) != hipSuccess) return e;
+  decode_splitk_kernel<T, D, HMAX><<<p.grid, kWaves * 64, 0, s>>>(p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if ((e = record_timing(a.timing_end, s)) != hipSuccess) return e;
-  if (p.nsplit_max <= 1) return hipSuccess;
-  merge_kernel<T, D><<<dim3(a.heads_q, a.batch), D, 0, s>>>(p);
+  const int nhs = (p.group + HMAX - 1) / HMAX;
+  merge_kernel<T, D, HMAX><<<dim3(a.heads_kv * nhs, a.batch), 256, 0, s>>>(p);
   return hipGetLastError();
+}
+
+// Query heads per workgroup for a GQA group size (the launch_d dispatch).
+int decode_hmax(const goda_decode_args& a) {
+  const int group = a.heads_q / a.heads_kv;
+  if (group <= 4) return 4;
+  if (group <= 8 || a.head_dim > 128) return 8;
+  return 16;
 }
 
 template <typename T, int D>
 hipError_t launch_d(const DecodeParams& p, hipStream_t s) {
   if (p.group <= 4) return launch_hd<T, D, 4>(p, s);
-  if (p.group <= 8 || D > 128) return launch_hd<T, D, 8>(p, s);
-  return launch_hd<T, D, 16>(p, s);
+  if constexpr (D > 128) {
+    return launch_hd<T, D, 8>(p, s);
+  } else {
+    if (p.group <= 8) return launch_hd<T, D, 8>(p, s);
+    return launch_hd<T, D, 16>(p, s);
+  }
 }
 
 template <typename T>
@@ -403,22 +641,22 @@ bool decode_mfma_supported(const goda_decode_args& a) {
   return a.head_dim == 128 || a.head_dim == 256;
 }
 
-int decode_default_split(const goda_decode_args& a) {
-  // Aim for ~4096 workgroups with the cache assumed half full; splits are a
-  // multiple of one workgroup step (4 waves x 16 keys).
+int64_t decode_slots(const goda_decode_args& a) {
+  // Ranges are at most ceil(total / split), or with the balanced default at
+  // most min(grid, ceil(total / kMinRange)); total <= units * batch * max_seqlen.
   const int group = a.heads_q / a.heads_kv;
-  const int hmax = group <= 4 ? 4 : (group <= 8 || a.head_dim > 128) ? 8 : 16;
-  const int64_t units = (int64_t)a.batch * a.heads_kv * ((group + hmax - 1) / hmax);
-  const int64_t keys = units * ((int64_t)a.max_seqlen / 2 + 1);
-  int split = 256;
-  while (split < 4096 && keys / split > 4096) split *= 2;
-  return split;
+  const int hmax = decode_hmax(a);
+  const int64_t units = (int64_t)a.heads_kv * ((group + hmax - 1) / hmax);
+  const int64_t tmax = units * a.batch * (int64_t)a.max_seqlen;
+  const int64_t per = a.split_size > 0 ? a.split_size : kMinRange;
+  int64_t ranges = (tmax + per - 1) / per;
+  if (a.split_size <= 0) ranges = std::min<int64_t>(ranges, kMaxGrid);
+  return 2 * ranges;
 }
 
-int64_t decode_workspace_bytes(const goda_decode_args& a, int split) {
-  const int64_t nsplit = ((int64_t)a.max_seqlen + split - 1) / split;
-  if (nsplit <= 1) return 0;
-  return (int64_t)a.batch * a.heads_q * nsplit * (a.head_dim + 1) * 4;
+int64_t decode_workspace_bytes(const goda_decode_args& a) {
+  if (a.batch <= 0 || a.max_seqlen <= 0) return 0;
+  return decode_slots(a) * decode_hmax(a) * (a.head_dim + 1) * (int64_t)sizeof(float);
 }
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {

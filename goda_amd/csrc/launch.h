@@ -24,8 +24,9 @@ struct DecodeParams {
   goda_decode_args a;
   int group;
   float scale_log2;
-  int split;          // keys per split
-  int nsplit_max;     // ceil(max_seqlen / split)
+  int split;          // keys per work range; 0: balanced over the grid
+  int grid;           // persistent workgroups (set by the launcher)
+  int64_t nslots;     // partial slots in the workspace
 };
 
 // Generic (VALU) prefill: any dtype, head_dim in {64,128,256}.
@@ -39,8 +40,8 @@ hipError_t launch_prefill_mfma(const PrefillParams& p, hipStream_t s);
 
 // Split-K decode for bf16/fp16; fp32 decode goes through the generic prefill.
 bool decode_mfma_supported(const goda_decode_args& a);
-int decode_default_split(const goda_decode_args& a);
-int64_t decode_workspace_bytes(const goda_decode_args& a, int split);
+int64_t decode_slots(const goda_decode_args& a);
+int64_t decode_workspace_bytes(const goda_decode_args& a);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s);
 
 hipError_t launch_kv_append(const goda_kv_append_args& a, hipStream_t s);

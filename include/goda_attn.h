@@ -119,7 +119,8 @@ typedef struct goda_decode_args {
   int32_t head_dim;
   int32_t max_seqlen;   /* rows of the cache (Lmax) */
   int32_t window_left;  /* -1: unlimited */
-  int32_t split_size;   /* keys per split-K chunk; 0 = library default */
+  int32_t split_size;   /* keys per work range (multiple of 64); 0 = the visible
+                           keys of all sequences spread evenly over the GPU */
   float softmax_scale;
   int32_t reserved0;
 
@@ -201,7 +202,9 @@ int32_t goda_attn_prefill_fwd(const goda_prefill_args* args, void* stream);
 int64_t goda_attn_decode_workspace_size(const goda_decode_args* args);
 
 /* One-token decode over a contiguous KV cache with per-sequence lengths:
- * split-K partial softmax over chunks of the cache, merged by log-sum-exp.
+ * the visible keys of all sequences and KV heads are cut into equal ranges
+ * for a persistent grid (split-K), partial softmax results of a sequence that
+ * spans several ranges are merged by log-sum-exp.
  * Replaces FlashAttention._attention_with_kvcache for q_len == 1
  * (mint/nn/flashattn.py:174-219); its argument set mirrors the
  * flash_attn_with_kvcache call at mint/nn/flashattn.py:191-200. */

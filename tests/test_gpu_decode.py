@@ -93,6 +93,28 @@ def test_decode_bhtd_layout(dtype):
     _decode_case(len(lens), 8, 2, 128, 1024, lens, dtype, split=256, layout="bhtd", seed=9)
 
 
+@pytest.mark.parametrize("split", [0, 64])
+def test_decode_ragged_many_sequences(split):
+    """Balanced split-K over a batch wider than one 64-sequence scan block,
+    with runs of empty sequences and one long sequence among short ones:
+    ranges then cross many sequence boundaries, and with split 64 there are
+    more ranges than workgroups."""
+    g = torch.Generator().manual_seed(7)
+    lens = torch.randint(1, 90, (150,), generator=g)
+    lens[10:30] = 0
+    lens[70] = 1500
+    lens[149] = 0
+    _decode_case(150, 8, 2, 128, 1536, lens.tolist(), torch.bfloat16, split=split, seed=11)
+
+
+def test_decode_all_empty():
+    b, hq, hkv, d = 70, 8, 2, 128
+    q = _rand((b, hq, d), torch.bfloat16, 1).to(DEV)
+    kc = torch.zeros(b, 32, hkv, d, dtype=torch.bfloat16, device=DEV)
+    o, lse = ops.attention_decode(q, kc, kc, torch.zeros(b, dtype=torch.int32, device=DEV), return_lse=True)
+    assert torch.all(o.cpu() == 0) and torch.all(torch.isneginf(lse.cpu()))
+
+
 def test_decode_zero_length():
     lens = [0, 10]
     q = _rand((2, 4, 128), torch.bfloat16, 1)
