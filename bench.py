@@ -225,6 +225,21 @@ def cpu_baseline_decode(w, nseq: int = 8, reps: int = 3):
     }
 
 
+def _committed_traffic(name: str):
+    """HBM bytes per launch of a kernel, from the committed rocprofv3 counter
+    summary profiles/<name> (FETCH_SIZE and WRITE_SIZE passes, each scaled by
+    what the counter reads for a copy kernel of known size); None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return {"bytes": float(line.split(":", 1)[1]), "source": f"profiles/{name}"}
+    except OSError:
+        pass
+    return None
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -296,6 +311,8 @@ def main() -> int:
 
     peak_tf = wl.BF16_PEAK_TFLOPS
     peak_bw = wl.HBM_PEAK_GBPS
+    tr_pf = _committed_traffic("prefill_fa_cfg2_hbm_traffic.md")
+    tr_dec = _committed_traffic("decode_splitk_cfg4_hbm_traffic.md")
     line: dict = {"metric": METRIC, "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True,
                   "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded N(0,1)*0.5)"}
     if "cfg2" in out:
@@ -324,7 +341,8 @@ def main() -> int:
                 "peak": peak_tf,
                 "unit": "TFLOP/s",
                 "frac": round(p2["kernel_tflops"] / peak_tf, 4),
-                "traffic": None,
+                "traffic": tr_pf["bytes"] if tr_pf else None,
+                "traffic_source": tr_pf["source"] if tr_pf else None,
                 "kernel_ms": round(p2["kernel_ms"], 4),
                 "flops_per_launch": p2["flops"],
             },
@@ -346,7 +364,8 @@ def main() -> int:
                 "peak": peak_bw,
                 "unit": "GB/s",
                 "frac": round(d4["kernel_gbps"] / peak_bw, 4),
-                "traffic": None,
+                "traffic": tr_dec["bytes"] if tr_dec else None,
+                "traffic_source": tr_dec["source"] if tr_dec else None,
                 "kernel_ms": round(d4["kernel_ms"], 4),
                 "bytes_per_launch": d4["bytes"],
             },
