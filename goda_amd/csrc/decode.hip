@@ -162,6 +162,21 @@ struct Segment {
   int64_t slot;    // workspace slot of a partial segment
 };
 
+// The launch parameters, re-read from the kernel argument segment (scalar
+// loads) wherever this is called, instead of being held in scalar registers
+// across the segment loop, which spills them. The kernel's only argument sits
+// at offset 0 of that segment.
+__device__ __forceinline__ const DecodeParams& reload_params() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __attribute__((address_space(4))) const DecodeParams* ParamsPtr;
+  ParamsPtr pp = (ParamsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pp));
+  return *pp;
+#else
+  return *static_cast<const DecodeParams*>(nullptr);  // host pass: never executed
+#endif
+}
+
 template <int D, int HMAX>
 struct DecodeSmem {
   float p[kWaves][kChunk][16];
@@ -175,13 +190,7 @@ struct DecodeSmem {
 // workgroup barrier so the LDS can be reused by the next segment.
 template <typename T, int D, int HMAX>
 __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segment& sg) {
-  // The launch parameters are re-read from the kernel argument segment for
-  // every segment (scalar loads) rather than held in scalar registers across
-  // the segment loop, which would spill them.
-  typedef __attribute__((address_space(4))) const DecodeParams* ParamsPtr;
-  ParamsPtr pp = (ParamsPtr)__builtin_amdgcn_kernarg_segment_ptr();
-  asm volatile("" : "+s"(pp));
-  const DecodeParams& p = *pp;
+  const DecodeParams& p = reload_params();
   typedef typename V8<T>::t v8;
   constexpr int KS = D / 32;    // k-steps of the 16x16x32 score MFMA
   constexpr int CPL = D / 128;  // 8-element head-dim chunks per lane in PV
@@ -417,7 +426,7 @@ template <int D, int HMAX>
 constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : 1;
 
 // The kernel's only argument sits at offset 0 of the kernel argument segment
-// (run_segment reads it from there).
+// (reload_params reads it from there).
 template <typename T, int D, int HMAX>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<D, HMAX>)))
 decode_splitk_kernel(const DecodeParams p) {
