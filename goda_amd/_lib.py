@@ -17,7 +17,7 @@ from pathlib import Path
 _LIB_ENV = "GODA_ATTN_LIB"
 _DEFAULT = Path(__file__).resolve().parent / "lib" / "libgoda_attn.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -162,15 +162,43 @@ class KvAppendArgs(ctypes.Structure):
     ]
 
 
+class PrefillGrads(ctypes.Structure):
+    _fields_ = [
+        ("d_o", _vp),
+        ("do_stride_b", _i64),
+        ("do_stride_t", _i64),
+        ("do_stride_h", _i64),
+        ("dq", _vp),
+        ("dq_stride_b", _i64),
+        ("dq_stride_t", _i64),
+        ("dq_stride_h", _i64),
+        ("dk", _vp),
+        ("dk_stride_b", _i64),
+        ("dk_stride_t", _i64),
+        ("dk_stride_h", _i64),
+        ("dv", _vp),
+        ("dv_stride_b", _i64),
+        ("dv_stride_t", _i64),
+        ("dv_stride_h", _i64),
+        ("workspace", _vp),
+        ("workspace_bytes", _i64),
+        ("timing_begin", _vp),
+        ("timing_end", _vp),
+    ]
+
+
 # Every symbol the header declares, with its ctypes signature.
 SYMBOLS = {
     "goda_attn_abi_version": (_i32, []),
     "goda_attn_sizeof_prefill_args": (_i64, []),
     "goda_attn_sizeof_decode_args": (_i64, []),
     "goda_attn_sizeof_kv_append_args": (_i64, []),
+    "goda_attn_sizeof_prefill_grads": (_i64, []),
     "goda_attn_last_error": (ctypes.c_char_p, []),
     "goda_attn_prefill_workspace_size": (_i64, [ctypes.POINTER(PrefillArgs)]),
     "goda_attn_prefill_fwd": (_i32, [ctypes.POINTER(PrefillArgs), _vp]),
+    "goda_attn_prefill_bwd_workspace_size": (_i64, [ctypes.POINTER(PrefillArgs)]),
+    "goda_attn_prefill_bwd": (_i32, [ctypes.POINTER(PrefillArgs), ctypes.POINTER(PrefillGrads), _vp]),
     "goda_attn_decode_workspace_size": (_i64, [ctypes.POINTER(DecodeArgs)]),
     "goda_attn_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "goda_attn_kv_append": (_i32, [ctypes.POINTER(KvAppendArgs), _vp]),
@@ -219,6 +247,7 @@ def load() -> ctypes.CDLL:
             (PrefillArgs, lib.goda_attn_sizeof_prefill_args),
             (DecodeArgs, lib.goda_attn_sizeof_decode_args),
             (KvAppendArgs, lib.goda_attn_sizeof_kv_append_args),
+            (PrefillGrads, lib.goda_attn_sizeof_prefill_grads),
         ):
             if ctypes.sizeof(struct) != fn():
                 raise RuntimeError(

@@ -99,6 +99,7 @@ int32_t goda_attn_abi_version(void) { return GODA_ATTN_ABI_VERSION; }
 int64_t goda_attn_sizeof_prefill_args(void) { return sizeof(goda_prefill_args); }
 int64_t goda_attn_sizeof_decode_args(void) { return sizeof(goda_decode_args); }
 int64_t goda_attn_sizeof_kv_append_args(void) { return sizeof(goda_kv_append_args); }
+int64_t goda_attn_sizeof_prefill_grads(void) { return sizeof(goda_prefill_grads); }
 
 const char* goda_attn_last_error(void) { return g_last_error.c_str(); }
 
@@ -123,6 +124,35 @@ int32_t goda_attn_prefill_fwd(const goda_prefill_args* a, void* stream) {
     return hip_status(goda::launch_prefill_mfma(p, s), "prefill_fwd");
   }
   return hip_status(goda::launch_prefill_generic(p, s), "prefill_fwd");
+}
+
+int64_t goda_attn_prefill_bwd_workspace_size(const goda_prefill_args* a) {
+  const int32_t st = check_prefill(a, false);
+  if (st != GODA_OK) return st;
+  return goda::prefill_bwd_workspace_bytes(*a);
+}
+
+int32_t goda_attn_prefill_bwd(const goda_prefill_args* a, const goda_prefill_grads* g, void* stream) {
+  const int32_t st = check_prefill(a, false);
+  if (st != GODA_OK) return st;
+  if (!g) return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: grads is NULL");
+  if (a->batch == 0 || (a->seqlen_q == 0 && a->seqlen_k == 0)) return ok();
+  if (!a->q || !a->k || !a->v || !a->o || !g->d_o || !g->dq || !g->dk || !g->dv)
+    return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: NULL tensor pointer");
+  if (!a->lse) return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: the forward's lse is required");
+  const int64_t need = goda::prefill_bwd_workspace_bytes(*a);
+  if (need > 0 && (!g->workspace || g->workspace_bytes < need))
+    return fail(GODA_ERR_WORKSPACE, "prefill_bwd: workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)g->workspace_bytes);
+  goda::BwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.a = *a;
+  p.g = *g;
+  p.group = a->heads_q / a->heads_kv;
+  p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+  p.delta_rows = (int64_t)a->batch * a->seqlen_q;
+  p.delta = reinterpret_cast<float*>(g->workspace);
+  return hip_status(goda::launch_prefill_bwd(p, reinterpret_cast<hipStream_t>(stream)), "prefill_bwd");
 }
 
 int64_t goda_attn_decode_workspace_size(const goda_decode_args* a) {

@@ -82,6 +82,30 @@ __device__ __forceinline__ void st_vec(T* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// Four consecutive elements as fp32, and back.
+template <typename T>
+__device__ __forceinline__ void load4f(const T* p, float (&out)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[j] = Elem<T>::to_f32(p[j]);
+}
+template <>
+__device__ __forceinline__ void load4f<float>(const float* p, float (&out)[4]) {
+  const f32x4 v = ld_vec<f32x4>(p);
+  out[0] = v[0];
+  out[1] = v[1];
+  out[2] = v[2];
+  out[3] = v[3];
+}
+template <typename T>
+__device__ __forceinline__ void store4f(T* p, const float (&v)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = Elem<T>::from_f32(v[j]);
+}
+template <>
+__device__ __forceinline__ void store4f<float>(float* p, const float (&v)[4]) {
+  st_vec<f32x4>(p, f32x4{v[0], v[1], v[2], v[3]});
+}
+
 // Per-sequence geometry shared by every kernel: row offsets of sequence b in
 // q/k storage and its query / key counts.
 struct SeqGeom {

@@ -29,6 +29,21 @@ struct DecodeParams {
   int64_t nslots;     // partial slots in the workspace
 };
 
+// Launch-ready backward parameters.
+struct BwdParams {
+  goda_prefill_args a;   // the forward's arguments (o, lse: its outputs)
+  goda_prefill_grads g;
+  int group;
+  float scale_log2;
+  int64_t delta_rows;    // row stride of the delta buffer: batch * seqlen_q
+  float* delta;          // fp32 [heads_q, delta_rows]: rowsum(dO * O)
+};
+
+// Backward: workspace bytes and the launch (generic VALU kernels for every
+// dtype; MFMA kernels for bf16/fp16 where an instance exists).
+int64_t prefill_bwd_workspace_bytes(const goda_prefill_args& a);
+hipError_t launch_prefill_bwd(const BwdParams& p, hipStream_t s);
+
 // Generic (VALU) prefill: any dtype, head_dim in {64,128,256}.
 hipError_t launch_prefill_generic(const PrefillParams& p, hipStream_t s);
 

@@ -13,7 +13,9 @@ and extend it compatibly:
     K) and fp32 slopes [Hq];
   - any T (the reference requires T to be a multiple of its block size).
 The forward saves O and the log-sum-exp M (natural log, fp32 [B, H, T]) like
-the reference (:571-575).
+the reference (:571-575); the backward returns (dQ, dK, dV, None, ...) from
+them through `goda_attn_prefill_bwd` (:577-658), with dK/dV in K's and V's
+head count (summed over each KV head's query group).
 """
 
 from __future__ import annotations
@@ -45,17 +47,26 @@ class _FlashAttentionBase(torch.autograd.Function):
         )
         O = o.transpose(1, 2)  # noqa: N806  [B, H, T, D] view of a [B, T, H, D] buffer
         ctx.save_for_backward(Q, K, V, O, lse)
-        ctx.causal = bool(causal)
-        ctx.tau = float(tau)
-        ctx.window_left = int(window_left)
-        ctx.has_extras = rope or alibi_slopes is not None
+        ctx.options = dict(
+            causal=bool(causal),
+            softmax_scale=float(tau),
+            window_left=int(window_left),
+            alibi_slopes=alibi_slopes,
+            rope_cos=rope_cos,
+            rope_sin=rope_sin,
+            rope_q=rope,
+            rope_k=rope,
+        )
         return O
 
     @staticmethod
     def backward(ctx, dO):  # noqa: N803
-        raise NotImplementedError(
-            "goda_amd: the HIP backward kernels are not built yet; use the forward in no_grad/eval"
+        Q, K, V, O, lse = ctx.saved_tensors  # noqa: N806
+        dq, dk, dv = ops.attention_prefill_bwd(
+            Q.transpose(1, 2), K.transpose(1, 2), V.transpose(1, 2), O.transpose(1, 2), lse, dO.transpose(1, 2),
+            **ctx.options,
         )
+        return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None, None, None, None
 
 
 class FlashAttentionGQAKernel(_FlashAttentionBase):

@@ -13,6 +13,10 @@ base_attn_mask, doc_ids)` keeps the reference signature and its results
   - the KV-cache path appends on the device at each sequence's own length
     (no `.item()` sync, :202) and decodes with the split-K kernel.
 
+Without a KV cache the attention is differentiable: under autograd the
+backward runs on the HIP backward kernels (goda's training path,
+pretrain.py / sfttrain.py). The KV-cache path is inference only.
+
 Extra keyword arguments fuse the positional encoding into the kernels:
 `rope=(cos, sin)` fp32 tables with `start_pos` (q and k are then passed
 UNROTATED), or `alibi_slopes` [Hq]. There is no SDPA or CPU fallback:
@@ -24,7 +28,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ... import ops
+from ... import autograd, ops
 from ..kvcache.base import KVCache
 
 
@@ -90,7 +94,7 @@ class FlashAttention(nn.Module):
                 # attention in goda too, mint/nn/attn.py:60).
                 q, k = _rotate(q, rope, start_pos), _rotate(k, rope, start_pos)
             cu, max_len = _segments(doc_ids)
-            o = ops.attention_prefill(
+            o = autograd.attention_prefill(
                 q.reshape(b * t, hq, d),
                 k.reshape(b * t, hkv, d),
                 v.reshape(b * t, hkv, d),
@@ -107,8 +111,8 @@ class FlashAttention(nn.Module):
         if rope is not None:
             kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True, rope_k=True,
                       rope_q_offset=start_pos, rope_k_offset=start_pos)
-        return ops.attention_prefill(q, k, v, causal=causal, window_left=window_left,
-                                     alibi_slopes=alibi_slopes, **kw)
+        return autograd.attention_prefill(q, k, v, causal=causal, window_left=window_left,
+                                          alibi_slopes=alibi_slopes, **kw)
 
     # mint/nn/flashattn.py:174-219
     def _attention_with_kvcache(self, q, k, v, kv_cache: KVCache, *, causal, window_left, rope, alibi_slopes):

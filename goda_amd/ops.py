@@ -110,7 +110,33 @@ def attention_prefill(*args, **kwargs):
     return plan_prefill(*args, **kwargs)()
 
 
-def plan_prefill(
+def plan_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **kwargs):
+    """Validate the arguments of `goda_attn_prefill_fwd`, allocate outputs
+    and workspace, and return the `Launch` that runs it.
+
+    Semantics are those of goda's eager path (mint/nn/flashattn.py:221-273):
+    GQA head mapping h -> h // (Hq/Hkv), bottom-right causal alignment, left
+    window only with causal (or a single query), ALiBi as
+    slope_h * (j - i_abs), RoPE as mint/nn/pos.py:90-112 using the given
+    fp32 cos/sin tables. Returns `o` (and `lse` fp32 if `return_lse`).
+    Keyword arguments: see `_prefill_args`.
+    """
+    a, keep, o, lse = _prefill_args(q, k, v, **kwargs)
+    lib = _lib.load()
+    need = lib.goda_attn_prefill_workspace_size(ctypes.byref(a))
+    if need < 0:
+        _lib.check(int(need))
+    ws = None
+    if need > 0:
+        ws = torch.empty(int(need), dtype=torch.uint8, device=q.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
+    # The plan keeps every tensor the struct points to alive. Once a plan is
+    # dropped, the caching allocator only reuses that memory for work
+    # ordered after the launch on this stream.
+    return Launch("goda_attn_prefill_fwd", a, keep + (ws,), (o, lse) if lse is not None else o)
+
+
+def _prefill_args(
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
@@ -132,16 +158,11 @@ def plan_prefill(
     seqused_k: torch.Tensor | None = None,
     return_lse: bool = False,
     out: torch.Tensor | None = None,
+    lse_in: torch.Tensor | None = None,
 ):
-    """Validate the arguments of `goda_attn_prefill_fwd`, allocate outputs
-    and workspace, and return the `Launch` that runs it.
-
-    Semantics are those of goda's eager path (mint/nn/flashattn.py:221-273):
-    GQA head mapping h -> h // (Hq/Hkv), bottom-right causal alignment, left
-    window only with causal (or a single query), ALiBi as
-    slope_h * (j - i_abs), RoPE as mint/nn/pos.py:90-112 using the given
-    fp32 cos/sin tables. Returns `o` (and `lse` fp32 if `return_lse`).
-    """
+    """Validated `PrefillArgs` for q, k, v and the options, with `o` (`out`
+    or a new tensor) and `lse` (`lse_in`, a new tensor if `return_lse`, or
+    None). Returns (args, tensors to keep alive, o, lse); no workspace."""
     for name, t in (("q", q), ("k", k), ("v", v)):
         _require_gpu(name, t)
         _require_last_contig(name, t)
@@ -194,8 +215,15 @@ def plan_prefill(
     os_ = (0, o.stride(0), o.stride(1)) if varlen else (o.stride(0), o.stride(1), o.stride(2))
 
     lse = None
-    if return_lse:
-        lse = torch.empty((hq, q.shape[0]) if varlen else (batch, hq, tq), dtype=torch.float32, device=dev)
+    lse_shape = (hq, q.shape[0]) if varlen else (batch, hq, tq)
+    if lse_in is not None:
+        if tuple(lse_in.shape) != lse_shape or lse_in.dtype != torch.float32 or lse_in.device != dev:
+            raise ValueError(f"goda_amd: lse must be fp32 {lse_shape} on {dev}")
+        if lse_in.stride(-1) != 1:
+            raise ValueError("goda_amd: lse rows must be contiguous")
+        lse = lse_in
+    elif return_lse:
+        lse = torch.empty(lse_shape, dtype=torch.float32, device=dev)
 
     slopes = _f32_vec("alibi_slopes", alibi_slopes, hq, dev)
     cos, sin, rope_len = _rope_tables(rope_cos, rope_sin, d, dev)
@@ -227,19 +255,63 @@ def plan_prefill(
     a.rope_q, a.rope_k = int(bool(rope_q)), int(bool(rope_k))
     a.rope_q_offset, a.rope_k_offset = int(rope_q_offset), int(rope_k_offset)
 
+    keep = (q, k, v, o, lse, slopes, cos, sin, cu_q, cu_k, used)
+    return a, keep, o, lse
+
+
+def attention_prefill_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    d_o: torch.Tensor,
+    **kwargs,
+):
+    """Gradients (dq, dk, dv) of `attention_prefill` through
+    `goda_attn_prefill_bwd`, from the forward's o and lse and the upstream
+    gradient d_o. Takes the forward's own keyword arguments (causal, window,
+    ALiBi, RoPE, varlen, seqused_k, scale), so the scores are recomputed
+    exactly as the forward computed them. dk/dv have Hkv heads (summed over
+    each KV head's query group) and are zero for keys past seqused_k."""
+    kwargs.pop("return_lse", None)
+    kwargs.pop("out", None)
+    a, keep, o, lse = _prefill_args(q, k, v, out=o, lse_in=lse, **kwargs)
+    _require_gpu("d_o", d_o)
+    if d_o.shape != o.shape or d_o.dtype != o.dtype:
+        raise ValueError(f"goda_amd: d_o {tuple(d_o.shape)} {d_o.dtype} must match o {tuple(o.shape)} {o.dtype}")
+    if d_o.stride(-1) != 1:
+        d_o = d_o.contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    for name, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        _require_last_contig(name, t)
+    g = _lib.PrefillGrads()
+    varlen = q.dim() == 3
+
+    def strides(t):
+        return (0, t.stride(0), t.stride(1)) if varlen else (t.stride(0), t.stride(1), t.stride(2))
+
+    g.d_o = d_o.data_ptr()
+    g.do_stride_b, g.do_stride_t, g.do_stride_h = strides(d_o)
+    g.dq = dq.data_ptr()
+    g.dq_stride_b, g.dq_stride_t, g.dq_stride_h = strides(dq)
+    g.dk = dk.data_ptr()
+    g.dk_stride_b, g.dk_stride_t, g.dk_stride_h = strides(dk)
+    g.dv = dv.data_ptr()
+    g.dv_stride_b, g.dv_stride_t, g.dv_stride_h = strides(dv)
     lib = _lib.load()
-    need = lib.goda_attn_prefill_workspace_size(ctypes.byref(a))
+    need = lib.goda_attn_prefill_bwd_workspace_size(ctypes.byref(a))
     if need < 0:
         _lib.check(int(need))
     ws = None
     if need > 0:
-        ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
-        a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
-    # The plan keeps every tensor the struct points to alive. Once a plan is
-    # dropped, the caching allocator only reuses that memory for work
-    # ordered after the launch on this stream.
-    keep = (q, k, v, o, lse, ws, slopes, cos, sin, cu_q, cu_k, used)
-    return Launch("goda_attn_prefill_fwd", a, keep, (o, lse) if return_lse else o)
+        ws = torch.empty(int(need), dtype=torch.uint8, device=q.device)
+        g.workspace, g.workspace_bytes = ws.data_ptr(), int(need)
+    _lib.check(lib.goda_attn_prefill_bwd(ctypes.byref(a), ctypes.byref(g), _stream()))
+    del keep, ws  # the caching allocator orders reuse after this stream's work
+    return dq, dk, dv
 
 
 def attention_decode(*args, **kwargs):

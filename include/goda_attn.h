@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GODA_ATTN_ABI_VERSION 1
+#define GODA_ATTN_ABI_VERSION 2
 
 /* element types */
 #define GODA_DTYPE_F32 0
@@ -177,11 +177,36 @@ typedef struct goda_kv_append_args {
   int32_t reserved0;
 } goda_kv_append_args;
 
+/* Gradients for goda_attn_prefill_bwd. Every tensor uses the (b, t, h)
+ * element-stride convention of goda_prefill_args (b strides unused for
+ * varlen); the dtype is the forward's. */
+typedef struct goda_prefill_grads {
+  const void* d_o;      /* dL/dO, laid out like o */
+  int64_t do_stride_b, do_stride_t, do_stride_h;
+  void* dq;             /* dL/dq for the caller's (unrotated) q, like q */
+  int64_t dq_stride_b, dq_stride_t, dq_stride_h;
+  void* dk;             /* dL/dk, like k: heads_kv heads, each the sum over
+                           its query-head group; rows past a sequence's keys
+                           (seqused_k) are written as 0 */
+  int64_t dk_stride_b, dk_stride_t, dk_stride_h;
+  void* dv;             /* dL/dv, like v */
+  int64_t dv_stride_b, dv_stride_t, dv_stride_h;
+
+  void* workspace;      /* size from goda_attn_prefill_bwd_workspace_size */
+  int64_t workspace_bytes;
+
+  /* Optional hipEvent_t pair recorded around the gradient kernels (after the
+   * row-statistics pre-pass). NULL: not recorded. */
+  void* timing_begin;
+  void* timing_end;
+} goda_prefill_grads;
+
 /* ABI version and struct sizes, so that a binding can check its mirror. */
 int32_t goda_attn_abi_version(void);
 int64_t goda_attn_sizeof_prefill_args(void);
 int64_t goda_attn_sizeof_decode_args(void);
 int64_t goda_attn_sizeof_kv_append_args(void);
+int64_t goda_attn_sizeof_prefill_grads(void);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* goda_attn_last_error(void);
@@ -197,6 +222,20 @@ int64_t goda_attn_prefill_workspace_size(const goda_prefill_args* args);
  * FlashAttention._attention (mint/nn/flashattn.py:156-172, 221-273), including
  * the packed varlen call of mint/nn/flashattn.py:123-133 (cu_seqlens). */
 int32_t goda_attn_prefill_fwd(const goda_prefill_args* args, void* stream);
+
+/* Workspace needed by goda_attn_prefill_bwd for these forward arguments
+ * (bytes, >= 0), or a negative status if they are rejected. */
+int64_t goda_attn_prefill_bwd_workspace_size(const goda_prefill_args* fwd);
+
+/* Backward of goda_attn_prefill_fwd: dq, dk, dv from d_o and the forward's
+ * saved o and lse (fwd->o and fwd->lse must hold the forward's outputs for
+ * the same q, k, v and options; fwd->workspace is not used). With Hkv < Hq,
+ * dk/dv of a KV head sum its query heads' contributions. With RoPE the
+ * gradients are taken back through the rotation (dq, dk refer to the
+ * unrotated inputs). Replaces FlashAttentionGQAKernel.backward
+ * (kernels_/flash_attn_gqa/cuda.py:577-658: D = rowsum(dO * O), then
+ * dK/dV and dQ from P = exp(scale * q k^T - M)). */
+int32_t goda_attn_prefill_bwd(const goda_prefill_args* fwd, const goda_prefill_grads* grads, void* stream);
 
 /* Workspace needed by goda_attn_decode for these arguments (bytes, >= 0). */
 int64_t goda_attn_decode_workspace_size(const goda_decode_args* args);

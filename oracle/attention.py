@@ -369,3 +369,47 @@ def split_attention(q, k, v, splits: list[int], *, scale=None, dtype=torch.float
         ops.append(torch.einsum("hj,jhd->hd", p, v[s:e].to(dtype)))
         lps.append(lse)
     return merge_splits(torch.stack(ops), torch.stack(lps))
+
+
+# ---------------------------------------------------------------------------
+# gradients
+# ---------------------------------------------------------------------------
+def attention_grads(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    d_o: torch.Tensor,
+    *,
+    causal: bool,
+    window_size: tuple[int, int] = (-1, -1),
+    doc_ids: torch.Tensor | None = None,
+    alibi_slopes: torch.Tensor | None = None,
+    rope: tuple | None = None,
+    scale: float | None = None,
+    dtype=torch.float32,
+):
+    """(dq, dk, dv) of `attention` for the upstream gradient d_o [B, Tq, Hq, D].
+
+    Torch autograd through the same SDPA restatement: what goda's eager
+    training path back-propagates (mint/nn/flashattn.py:221-273 under
+    loss.backward()), and what FlashAttentionGQAKernel.backward
+    (kernels_/flash_attn_gqa/cuda.py:577-658) computes for Hq == Hkv. With
+    Hkv < Hq, dk/dv of a KV head sum its query heads (SDPA's enable_gqa).
+    `rope` = (cos, sin, q_positions, k_positions) rotates q and k first
+    (mint/nn/pos.py:90-112, applied before attention at mint/nn/attn.py:60),
+    so dq/dk refer to the unrotated inputs. Every query row must see at least
+    one key (SDPA returns NaN for a row with none).
+    """
+    qs = q.to("cpu", dtype).detach().requires_grad_(True)
+    ks = k.to("cpu", dtype).detach().requires_grad_(True)
+    vs = v.to("cpu", dtype).detach().requires_grad_(True)
+    qr, kr = qs, ks
+    if rope is not None:
+        cos, sin, qpos, kpos = rope
+        qr = apply_rope(qs, cos, sin, qpos)
+        kr = apply_rope(ks, cos, sin, kpos)
+    with torch.enable_grad():
+        o = attention(qr, kr, vs, causal=causal, window_size=window_size, doc_ids=doc_ids,
+                      alibi_slopes=alibi_slopes, scale=scale, dtype=dtype)
+        o.backward(d_o.to("cpu", dtype))
+    return qs.grad, ks.grad, vs.grad

@@ -89,3 +89,68 @@ def rope(x: np.ndarray, positions: np.ndarray, base: float, scale_factor: float 
             out[..., t, :, i] = x1 * c - x2 * s
             out[..., t, :, i + half] = x1 * s + x2 * c
     return out
+
+
+def attention_backward(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    d_o: np.ndarray,
+    *,
+    causal: bool,
+    window_left: int = -1,
+    slopes: np.ndarray | None = None,
+    doc_ids: np.ndarray | None = None,
+    scale: float | None = None,
+    plant: str | None = None,
+):
+    """Gradients (dq, dk, dv) of `attention` for upstream d_o, written out per
+    (row, key) pair in float64 — the FlashAttention-2 backward formulas that
+    kernels_/flash_attn_gqa/cuda.py:6-246 implements:
+        p_ij = exp(s_ij - lse_i),  delta_i = sum_d dO_i * o_i,
+        dv_j += p_ij dO_i,  ds_ij = p_ij (dO_i . v_j - delta_i),
+        dq_i += scale ds_ij k_j,  dk_j += scale ds_ij q_i,
+    with dk/dv of KV head h // group summed over the group's query heads.
+    Rows with no visible key contribute nothing.
+
+    `plant` is for the oracle's own tests only: "no_delta" drops delta_i,
+    "first_head_only" keeps only the first query head of each group in dk/dv.
+    """
+    q = q.astype(np.float64)
+    k = k.astype(np.float64)
+    v = v.astype(np.float64)
+    d_o = d_o.astype(np.float64)
+    b_, tq, hq, d = q.shape
+    tk, hkv = k.shape[1], k.shape[2]
+    group = hq // hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    o, lse = attention(q, k, v, causal=causal, window_left=window_left, slopes=slopes, doc_ids=doc_ids, scale=scale)
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    for b in range(b_):
+        for h in range(hq):
+            hk = h // group
+            keep_kv = plant != "first_head_only" or h % group == 0
+            for i in range(tq):
+                if not np.isfinite(lse[b, h, i]):
+                    continue
+                iabs = tk - tq + i
+                delta = 0.0 if plant == "no_delta" else float(np.dot(d_o[b, i, h], o[b, i, h]))
+                for j in range(tk):
+                    if causal and j > iabs:
+                        continue
+                    if window_left >= 0 and (causal or tq == 1) and iabs - j > window_left:
+                        continue
+                    if doc_ids is not None and doc_ids[b, i] != doc_ids[b, j]:
+                        continue
+                    s = float(np.dot(q[b, i, h], k[b, j, hk])) * scale
+                    if slopes is not None:
+                        s += float(slopes[h]) * (j - iabs)
+                    p = math.exp(s - lse[b, h, i])
+                    ds = p * (float(np.dot(d_o[b, i, h], v[b, j, hk])) - delta)
+                    dq[b, i, h] += scale * ds * k[b, j, hk]
+                    if keep_kv:
+                        dv[b, j, hk] += p * d_o[b, i, h]
+                        dk[b, j, hk] += scale * ds * q[b, i, h]
+    return dq, dk, dv

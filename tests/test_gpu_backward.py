@@ -1,0 +1,224 @@
+"""Backward parity: dq, dk, dv from goda_attn_prefill_bwd (through the C-ABI)
+against the CPU oracle's gradients (torch autograd through the SDPA
+restatement, pinned by tests/test_oracle.py against finite differences).
+
+Tolerance: the north-star bounds (1e-4 fp32, 2e-2 bf16/fp16) applied to the
+gradient error normalised by max(1, max |reference gradient|), because
+gradient magnitudes grow with the number of rows and group heads that feed
+one key.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from goda_amd import autograd, ops
+from goda_amd import workloads as wl
+from goda_amd.kernels_ import FlashAttentionGQAKernel, FlashAttentionMQAKernel
+from goda_amd.mint.nn import FlashAttention, GroupedQueryAttention, RoPE
+from oracle import attention as ref
+from oracle import brute
+from tests.helpers import TOL
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(shape, dtype, seed, std=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+def grad_err(x: torch.Tensor, x_ref: torch.Tensor) -> float:
+    x = x.to("cpu", torch.float32)
+    x_ref = x_ref.to("cpu", torch.float32)
+    return ((x - x_ref).abs().max() / max(1.0, x_ref.abs().max().item())).item()
+
+
+def _check(grads, refs, dtype, what=""):
+    for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
+        e = grad_err(g, r)
+        assert e <= TOL[dtype], f"{what} {name} err {e}"
+
+
+def _case(b, tq, tk, hq, hkv, d, dtype, *, causal, window=-1, alibi=False, rope=False, seed=0):
+    q = _rand((b, tq, hq, d), dtype, seed)
+    k = _rand((b, tk, hkv, d), dtype, seed + 1)
+    v = _rand((b, tk, hkv, d), dtype, seed + 2)
+    d_o = _rand((b, tq, hq, d), dtype, seed + 3, std=1.0)
+    kw, okw = {}, {}
+    if alibi:
+        slopes = torch.tensor(wl.alibi_slopes(hq), dtype=torch.float32)
+        kw["alibi_slopes"] = slopes.to(DEV)
+        okw["alibi_slopes"] = slopes
+    if rope:
+        cos, sin = wl.rope_tables(tk + 8, d, 10000.0)
+        kw.update(rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_q=True, rope_k=True)
+        okw["rope"] = (cos, sin, torch.arange(tk - tq, tk), torch.arange(tk))
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = ops.attention_prefill(qg, kg, vg, causal=causal, window_left=window, return_lse=True, **kw)
+    dq, dk, dv = ops.attention_prefill_bwd(qg, kg, vg, o, lse, d_o.to(DEV), causal=causal, window_left=window, **kw)
+    torch.cuda.synchronize()
+    refs = ref.attention_grads(q.float(), k.float(), v.float(), d_o.float(), causal=causal,
+                               window_size=(window, -1), **okw)
+    _check((dq, dk, dv), refs, dtype, f"b{b} tq{tq} tk{tk} h{hq}/{hkv} d{d} {dtype} causal={causal}")
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (6, 1)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_backward_shapes(dtype, d, hq, hkv, causal):
+    _case(2, 70, 70, hq, hkv, d, dtype, causal=causal, seed=d + hq)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("window", [0, 5, 40])
+def test_backward_window(dtype, window):
+    _case(2, 96, 96, 4, 2, 128, dtype, causal=True, window=window, seed=window)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_bottom_right_and_long(dtype):
+    _case(1, 50, 90, 8, 2, 128, dtype, causal=True, seed=5)  # Lq < Lk
+    _case(1, 300, 300, 4, 1, 128, dtype, causal=True, seed=6)  # several key blocks
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_alibi_and_rope(dtype):
+    _case(2, 64, 64, 8, 2, 128, dtype, causal=True, alibi=True, seed=7)
+    _case(2, 64, 64, 8, 2, 128, dtype, causal=True, rope=True, seed=8)
+    _case(1, 40, 72, 4, 1, 256, dtype, causal=True, rope=True, seed=9)
+
+
+def test_backward_rows_without_keys():
+    """Lq > Lk with causal: the first Lq - Lk rows see no key; their o is 0
+    and they contribute nothing (checked against the float64 brute force,
+    since SDPA itself returns NaN there)."""
+    b, tq, tk, hq, hkv, d = 1, 12, 8, 2, 1, 64
+    q, k, v = (_rand(s, torch.float32, i) for i, s in enumerate([(b, tq, hq, d), (b, tk, hkv, d), (b, tk, hkv, d)]))
+    d_o = _rand((b, tq, hq, d), torch.float32, 9, std=1.0)
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, return_lse=True)
+    dq, dk, dv = ops.attention_prefill_bwd(q.to(DEV), k.to(DEV), v.to(DEV), o, lse, d_o.to(DEV), causal=True)
+    bq, bk, bv = brute.attention_backward(q.numpy(), k.numpy(), v.numpy(), d_o.numpy(), causal=True)
+    for g, r in ((dq, bq), (dk, bk), (dv, bv)):
+        assert grad_err(g, torch.from_numpy(r)) <= 1e-4
+    assert torch.all(dq[:, : tq - tk].cpu() == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_varlen(dtype):
+    lens = [33, 1, 70, 12]
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    tot, hq, hkv, d = int(cu[-1]), 8, 2, 128
+    q, k, v = _rand((tot, hq, d), dtype, 1), _rand((tot, hkv, d), dtype, 2), _rand((tot, hkv, d), dtype, 3)
+    d_o = _rand((tot, hq, d), dtype, 4, std=1.0)
+    kw = dict(causal=True, cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(lens), max_seqlen_k=max(lens))
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), return_lse=True, **kw)
+    dq, dk, dv = ops.attention_prefill_bwd(q.to(DEV), k.to(DEV), v.to(DEV), o, lse, d_o.to(DEV), **kw)
+    for s, e in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        refs = ref.attention_grads(q[s:e][None].float(), k[s:e][None].float(), v[s:e][None].float(),
+                                   d_o[s:e][None].float(), causal=True)
+        _check((dq[s:e][None], dk[s:e][None], dv[s:e][None]), refs, dtype, f"segment {s}:{e}")
+
+
+def test_backward_seqused_k_zeroes_unused_keys():
+    b, tq, tk, hq, hkv, d = 2, 16, 64, 4, 2, 128
+    q, k, v = _rand((b, tq, hq, d), torch.float32, 1), _rand((b, tk, hkv, d), torch.float32, 2), _rand((b, tk, hkv, d), torch.float32, 3)
+    d_o = _rand((b, tq, hq, d), torch.float32, 4, std=1.0)
+    used = torch.tensor([40, 64], dtype=torch.int32)
+    kw = dict(causal=True, seqused_k=used.to(DEV))
+    o, lse = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), return_lse=True, **kw)
+    dq, dk, dv = ops.attention_prefill_bwd(q.to(DEV), k.to(DEV), v.to(DEV), o, lse, d_o.to(DEV), **kw)
+    for i, L in enumerate(used.tolist()):
+        refs = ref.attention_grads(q[i : i + 1], k[i : i + 1, :L], v[i : i + 1, :L], d_o[i : i + 1], causal=True)
+        _check((dq[i : i + 1], dk[i : i + 1, :L], dv[i : i + 1, :L]), refs, torch.float32, f"seq {i}")
+        assert torch.all(dk[i, L:].cpu() == 0) and torch.all(dv[i, L:].cpu() == 0)
+
+
+@pytest.mark.parametrize("cls", [FlashAttentionGQAKernel, FlashAttentionMQAKernel])
+def test_kernels_apply_backward(cls):
+    """kernels_/flash_attn_gqa/cuda.py:577-658: loss.backward() through
+    apply(Q, K, V, causal, tau) on [B, H, T, D] gives dQ, dK, dV."""
+    b, hq, hkv, t, d = 2, 8, 2, 80, 128
+    q = _rand((b, hq, t, d), torch.bfloat16, 1).to(DEV).requires_grad_(True)
+    k = _rand((b, hkv, t, d), torch.bfloat16, 2).to(DEV).requires_grad_(True)
+    v = _rand((b, hkv, t, d), torch.bfloat16, 3).to(DEV).requires_grad_(True)
+    d_o = _rand((b, hq, t, d), torch.bfloat16, 4, std=1.0)
+    o = cls.apply(q, k, v, True, 1.0 / math.sqrt(d))
+    o.backward(d_o.to(DEV))
+    refs = ref.attention_grads(q.detach().transpose(1, 2).float(), k.detach().transpose(1, 2).float(),
+                               v.detach().transpose(1, 2).float(), d_o.transpose(1, 2).float(), causal=True)
+    _check((q.grad.transpose(1, 2), k.grad.transpose(1, 2), v.grad.transpose(1, 2)), refs, torch.bfloat16)
+
+
+@pytest.mark.parametrize("with_rope", [False, True])
+def test_flashattention_doc_ids_backward(with_rope):
+    b, t, hq, hkv, d = 2, 64, 4, 2, 128
+    q = _rand((b, t, hq, d), torch.float32, 1)
+    k = _rand((b, t, hkv, d), torch.float32, 2)
+    v = _rand((b, t, hkv, d), torch.float32, 3)
+    d_o = _rand((b, t, hq, d), torch.float32, 4, std=1.0)
+    doc = torch.tensor([[0] * 20 + [1] * 30 + [2] * 14, [5] * 64])
+    kw, okw = {}, {}
+    if with_rope:
+        cos, sin = wl.rope_tables(t, d, 10000.0)
+        kw["rope"] = (cos.to(DEV), sin.to(DEV))
+        okw["rope"] = (cos, sin, torch.arange(t), torch.arange(t))
+    qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    o = FlashAttention()(qg, kg, vg, causal=True, doc_ids=doc.to(DEV), **kw)
+    o.backward(d_o.to(DEV))
+    refs = ref.attention_grads(q, k, v, d_o, causal=True, doc_ids=doc, **okw)
+    _check((qg.grad, kg.grad, vg.grad), refs, torch.float32)
+
+
+def test_autograd_entry_is_plain_forward_without_grad():
+    q = _rand((1, 16, 2, 64), torch.bfloat16, 1).to(DEV)
+    with torch.no_grad():
+        o = autograd.attention_prefill(q, q[:, :, :1], q[:, :, :1], causal=True)
+    assert o.grad_fn is None
+
+
+def test_gqa_layer_training_step_matches_cpu_reference():
+    """One training step of GroupedQueryAttention (mint/nn/attn.py:39-77) with
+    fused RoPE: parameter gradients from the HIP forward + backward equal those
+    of the same layer on the CPU with the oracle attention (fp32)."""
+    torch.manual_seed(0)
+    e, hq, hkv, d, t = 256, 4, 2, 128, 48
+    rope = RoPE(seq_len=64, head_dim=d, rope_base_theta=10000)
+    layer = GroupedQueryAttention(hq, hkv, d, e, rope, torch.float32)
+    with torch.no_grad():
+        for p_ in layer.parameters():
+            p_.normal_(0, 0.05)
+    x = torch.randn(2, t, e) * 0.5
+    gy = torch.randn(2, t, e)
+
+    layer_g = layer.to(DEV)
+    y = layer_g(x.to(DEV))
+    y.backward(gy.to(DEV))
+    grads = {n: p_.grad.detach().cpu() for n, p_ in layer_g.named_parameters()}
+
+    # CPU reference: the same computation with the oracle attention.
+    sd = {n: p_.detach().cpu().float().requires_grad_(True) for n, p_ in layer_g.named_parameters()}
+
+    def rms(z, scale):
+        return z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + scale)
+
+    qf = (x @ sd["wq.weight"].T).view(2, t, hq, d)
+    kf = (x @ sd["wk.weight"].T).view(2, t, hkv, d)
+    vf = (x @ sd["wv.weight"].T).view(2, t, hkv, d)
+    qf, kf = rms(qf, sd["q_norm.scale"]), rms(kf, sd["k_norm.scale"])
+    pos = torch.arange(t)
+    qf = ref.apply_rope(qf, rope.cos.cpu(), rope.sin.cpu(), pos)
+    kf = ref.apply_rope(kf, rope.cos.cpu(), rope.sin.cpu(), pos)
+    o = ref.attention(qf, kf, vf, causal=True)
+    y_ref = o.reshape(2, t, -1) @ sd["wo.weight"].T
+    y_ref.backward(gy)
+    for n, g in grads.items():
+        r = sd[n].grad
+        assert grad_err(g, r) <= 1e-4, f"{n}"

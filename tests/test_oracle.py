@@ -298,3 +298,115 @@ def test_planted_rope_pairing_is_caught():
     c, s = cos.to(F64)[:, None, :], sin.to(F64)[:, None, :]
     y_bad = torch.stack([xi[..., 0] * c - xi[..., 1] * s, xi[..., 0] * s + xi[..., 1] * c], -1).reshape(1, t, 1, d)
     assert not torch.allclose(y_bad, y_b, atol=1e-4)
+
+
+# ---------------------------------------------------------------------------
+# gradients: explicit FA2 backward (brute) vs finite differences, and the
+# autograd oracle vs the brute backward
+# ---------------------------------------------------------------------------
+def _loss_fd(fwd, args: list[np.ndarray], d_o: np.ndarray, h: float = 1e-5):
+    """Central finite differences of L = sum(o * d_o) w.r.t. every element of
+    every array in args (float64)."""
+    grads = []
+    for a_idx, a in enumerate(args):
+        g = np.zeros_like(a)
+        it = np.nditer(a, flags=["multi_index"])
+        for _ in it:
+            idx = it.multi_index
+            old = a[idx]
+            a[idx] = old + h
+            lp = float((fwd(*args) * d_o).sum())
+            a[idx] = old - h
+            lm = float((fwd(*args) * d_o).sum())
+            a[idx] = old
+            g[idx] = (lp - lm) / (2 * h)
+        grads.append(g)
+    return grads
+
+
+GRAD_CASES = [
+    # name, tq, tk, hq, hkv, d, kwargs
+    ("causal_gqa_bottom_right", 4, 6, 4, 2, 3, dict(causal=True)),
+    ("causal_window", 5, 5, 2, 1, 3, dict(causal=True, window_left=2)),
+    ("noncausal_alibi", 3, 4, 2, 1, 3, dict(causal=False, slopes=np.array([0.5, 0.25]))),
+    ("causal_empty_rows", 6, 4, 2, 1, 3, dict(causal=True)),
+    ("doc_ids", 5, 5, 2, 2, 3, dict(causal=True, doc_ids=np.array([[0, 0, 1, 1, 1]]))),
+]
+
+
+@pytest.mark.parametrize("name,tq,tk,hq,hkv,d,kw", GRAD_CASES, ids=[c[0] for c in GRAD_CASES])
+def test_brute_backward_matches_finite_differences(name, tq, tk, hq, hkv, d, kw):
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, tq, hq, d))
+    k = rng.standard_normal((1, tk, hkv, d))
+    v = rng.standard_normal((1, tk, hkv, d))
+    d_o = rng.standard_normal((1, tq, hq, d))
+    dq, dk, dv = brute.attention_backward(q, k, v, d_o, **kw)
+    fq, fk, fv = _loss_fd(lambda a, b_, c: brute.attention(a, b_, c, **kw)[0], [q, k, v], d_o)
+    assert np.abs(dq - fq).max() < 1e-7
+    assert np.abs(dk - fk).max() < 1e-7
+    assert np.abs(dv - fv).max() < 1e-7
+
+
+@pytest.mark.parametrize("plant", ["no_delta", "first_head_only"])
+def test_planted_backward_mistakes_are_caught(plant):
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((1, 4, 4, 3))
+    k = rng.standard_normal((1, 4, 2, 3))
+    v = rng.standard_normal((1, 4, 2, 3))
+    d_o = rng.standard_normal((1, 4, 4, 3))
+    kw = dict(causal=True)
+    dq, dk, dv = brute.attention_backward(q, k, v, d_o, plant=plant, **kw)
+    fq, fk, fv = _loss_fd(lambda a, b_, c: brute.attention(a, b_, c, **kw)[0], [q, k, v], d_o)
+    worst = max(np.abs(dq - fq).max(), np.abs(dk - fk).max(), np.abs(dv - fv).max())
+    assert worst > 1e-3
+
+
+@pytest.mark.parametrize(
+    "b,tq,tk,hq,hkv,d,causal,window,alibi",
+    [
+        (2, 6, 6, 4, 2, 8, True, -1, False),
+        (1, 5, 9, 4, 1, 8, True, 3, False),
+        (2, 7, 7, 2, 2, 8, False, -1, True),
+        (1, 4, 4, 8, 2, 16, True, -1, True),
+    ],
+)
+def test_autograd_oracle_matches_brute_backward(b, tq, tk, hq, hkv, d, causal, window, alibi):
+    q, k, v = _rand((b, tq, hq, d), 11), _rand((b, tk, hkv, d), 12), _rand((b, tk, hkv, d), 13)
+    d_o = _rand((b, tq, hq, d), 14)
+    slopes = torch.tensor(ref.alibi_slopes(hq), dtype=F64) if alibi else None
+    dq, dk, dv = ref.attention_grads(q, k, v, d_o, causal=causal, window_size=(window, -1), alibi_slopes=slopes, dtype=F64)
+    bq, bk, bv = brute.attention_backward(
+        q.numpy(), k.numpy(), v.numpy(), d_o.numpy(), causal=causal, window_left=window,
+        slopes=None if slopes is None else slopes.numpy(),
+    )
+    assert np.abs(dq.numpy() - bq).max() < 1e-10
+    assert np.abs(dk.numpy() - bk).max() < 1e-10
+    assert np.abs(dv.numpy() - bv).max() < 1e-10
+
+
+def test_autograd_oracle_through_rope_matches_finite_differences():
+    """dq, dk refer to the unrotated inputs: the rotation's transpose is applied
+    to the gradients of the rotated rows (checked against finite differences of
+    brute-force attention over brute-force RoPE)."""
+    tq, tk, hq, hkv, d, base = 3, 5, 2, 1, 4, 10000.0
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((1, tq, hq, d))
+    k = rng.standard_normal((1, tk, hkv, d))
+    v = rng.standard_normal((1, tk, hkv, d))
+    d_o = rng.standard_normal((1, tq, hq, d))
+    qpos, kpos = np.arange(tk - tq, tk) + 3, np.arange(tk) + 3
+    cos, sin = ref.rope_tables(16, d, base)
+    dq, dk, dv = ref.attention_grads(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), torch.from_numpy(d_o), causal=True,
+        rope=(cos.double(), sin.double(), torch.from_numpy(qpos), torch.from_numpy(kpos)), dtype=F64,
+    )
+
+    def fwd(a, b_, c):
+        return brute.attention(brute.rope(a, qpos, base), brute.rope(b_, kpos, base), c, causal=True)[0]
+
+    fq, fk, fv = _loss_fd(fwd, [q, k, v], d_o)
+    # the fp32 cos/sin tables limit agreement to ~1e-7
+    assert np.abs(dq.numpy() - fq).max() < 1e-5
+    assert np.abs(dk.numpy() - fk).max() < 1e-5
+    assert np.abs(dv.numpy() - fv).max() < 1e-7
