@@ -17,7 +17,7 @@ from pathlib import Path
 _LIB_ENV = "GODA_ATTN_LIB"
 _DEFAULT = Path(__file__).resolve().parent / "lib" / "libgoda_attn.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -77,7 +77,9 @@ class PrefillArgs(ctypes.Structure):
         ("rope_k", _i32),
         ("rope_q_offset", _i32),
         ("rope_k_offset", _i32),
-        ("reserved0", _i32),
+        ("norm_eps", _f32),
+        ("q_norm_weight", _vp),
+        ("k_norm_weight", _vp),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
         ("timing_begin", _vp),
@@ -120,7 +122,8 @@ class DecodeArgs(ctypes.Structure):
         ("rope_len", _i32),
         ("rope_q", _i32),
         ("rope_q_offset", _i32),
-        ("reserved1", _i32),
+        ("norm_eps", _f32),
+        ("q_norm_weight", _vp),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
         ("timing_begin", _vp),
@@ -158,7 +161,8 @@ class KvAppendArgs(ctypes.Structure):
         ("rope_len", _i32),
         ("rope_k", _i32),
         ("rope_k_offset", _i32),
-        ("reserved0", _i32),
+        ("norm_eps", _f32),
+        ("k_norm_weight", _vp),
     ]
 
 

@@ -60,6 +60,8 @@ int32_t check_prefill(const goda_prefill_args* a, bool need_ptrs) {
     return fail(GODA_ERR_INVALID_ARG, "prefill: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
   if (!(a->softmax_scale > 0.f))
     return fail(GODA_ERR_INVALID_ARG, "prefill: softmax_scale must be positive (got %g)", (double)a->softmax_scale);
+  if ((a->q_norm_weight || a->k_norm_weight) && !(a->norm_eps >= 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "prefill: norm_eps must be >= 0 (got %g)", (double)a->norm_eps);
   if (a->batch == 0 || a->seqlen_q == 0) return GODA_OK;
   if (need_ptrs && (!a->q || !a->k || !a->v || !a->o))
     return fail(GODA_ERR_INVALID_ARG, "prefill: NULL tensor pointer");
@@ -136,6 +138,8 @@ int32_t goda_attn_prefill_bwd(const goda_prefill_args* a, const goda_prefill_gra
   const int32_t st = check_prefill(a, false);
   if (st != GODA_OK) return st;
   if (!g) return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: grads is NULL");
+  if (a->q_norm_weight || a->k_norm_weight)
+    return fail(GODA_ERR_UNSUPPORTED, "prefill_bwd: the fused QK-RMSNorm is forward only (keep the norm outside for training)");
   if (a->batch == 0 || (a->seqlen_q == 0 && a->seqlen_k == 0)) return ok();
   if (!a->q || !a->k || !a->v || !a->o || !g->d_o || !g->dq || !g->dk || !g->dv)
     return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: NULL tensor pointer");
@@ -180,6 +184,8 @@ int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
                 a->split_size);
   if (!(a->softmax_scale > 0.f))
     return fail(GODA_ERR_INVALID_ARG, "decode: softmax_scale must be positive (got %g)", (double)a->softmax_scale);
+  if (a->q_norm_weight && !(a->norm_eps >= 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "decode: norm_eps must be >= 0 (got %g)", (double)a->norm_eps);
   if (a->batch == 0) return ok();
   if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->cache_seqlens)
     return fail(GODA_ERR_INVALID_ARG, "decode: NULL tensor pointer");
@@ -246,6 +252,8 @@ int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
   pa.rope_len = a->rope_len;
   pa.rope_q = a->rope_q;
   pa.rope_q_offset = a->rope_q_offset;
+  pa.q_norm_weight = a->q_norm_weight;
+  pa.norm_eps = a->norm_eps;
   pa.timing_begin = a->timing_begin;
   pa.timing_end = a->timing_end;
   goda::PrefillParams p = make_prefill_params(&pa);
@@ -258,6 +266,10 @@ int32_t goda_attn_kv_append(const goda_kv_append_args* a, void* stream) {
   if (a->batch < 0 || a->seqlen_new < 0 || a->heads_kv <= 0 || a->head_dim <= 0 || a->head_dim % 2 != 0)
     return fail(GODA_ERR_INVALID_ARG, "kv_append: bad sizes (batch %d, seqlen_new %d, heads_kv %d, head_dim %d)",
                 a->batch, a->seqlen_new, a->heads_kv, a->head_dim);
+  if (!head_dim_ok(a->head_dim))
+    return fail(GODA_ERR_UNSUPPORTED, "kv_append: head_dim %d not in {64, 128, 256}", a->head_dim);
+  if (a->k_norm_weight && !(a->norm_eps >= 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "kv_append: norm_eps must be >= 0 (got %g)", (double)a->norm_eps);
   if (a->batch == 0) return ok();
   if (!a->k_new || !a->v_new || !a->k_cache || !a->v_cache || !a->cache_seqlens)
     return fail(GODA_ERR_INVALID_ARG, "kv_append: NULL tensor pointer");

@@ -82,6 +82,10 @@ __device__ __forceinline__ void st_vec(T* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// goda's RMSNorm (mint/nn/norm.py:17-27) of a row with sum of squares `ss`
+// over `n` elements: x -> x * rms_scale(ss, n, eps) * (1 + w).
+__device__ __forceinline__ float rms_scale(float ss, int n, float eps) { return rsqrtf(ss / (float)n + eps); }
+
 // Four consecutive elements as fp32, and back.
 template <typename T>
 __device__ __forceinline__ void load4f(const T* p, float (&out)[4]) {

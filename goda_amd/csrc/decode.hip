@@ -50,6 +50,14 @@ __device__ __forceinline__ float group_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Sum over the same four lanes.
+__device__ __forceinline__ float group_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename T>
 struct V8;
 template <>
@@ -220,20 +228,46 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
                   (int64_t)(hq0 + min(l16, nh - 1)) * a.q_stride_h;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = head_ok ? ld_vec<v8>(qr + 32 * ks + 8 * kg) : v8{};
-    if (a.rope_q && head_ok) {
-      const int pos = qpos + a.rope_q_offset;
+    if (a.q_norm_weight || a.rope_q) {
+      // fp32 round trip: fused QK-RMSNorm, then RoPE, one rounding.
+      float xf[KS][8];
 #pragma unroll
-      for (int ks = 0; ks < KS / 2; ++ks) {
-        const int f0 = 32 * ks + 8 * kg;
-        const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + f0;
-        const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + f0;
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x1 = (float)qf[ks][e], x2 = (float)qf[ks + KS / 2][e];
-          qf[ks][e] = (T)(x1 * cs[e] - x2 * sn[e]);
-          qf[ks + KS / 2][e] = (T)(x1 * sn[e] + x2 * cs[e]);
+        for (int e = 0; e < 8; ++e) xf[ks][e] = (float)qf[ks][e];
+      if (a.q_norm_weight) {
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf(xf[ks][e], xf[ks][e], ss);
+        const float inv = rms_scale(group_sum(ss), D, a.norm_eps);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const float* w = a.q_norm_weight + 32 * ks + 8 * kg;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xf[ks][e] *= inv * (1.f + w[e]);
         }
       }
+      if (a.rope_q && head_ok) {
+        const int pos = qpos + a.rope_q_offset;
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ++ks) {
+          const int f0 = 32 * ks + 8 * kg;
+          const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + f0;
+          const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + f0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x1 = xf[ks][e], x2 = xf[ks + KS / 2][e];
+            xf[ks][e] = x1 * cs[e] - x2 * sn[e];
+            xf[ks + KS / 2][e] = x1 * sn[e] + x2 * cs[e];
+          }
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[ks][e] = (T)xf[ks][e];
     }
   }
   const float c = p.scale_log2;
@@ -590,40 +624,64 @@ hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // KV append: rows [pos_b, pos_b + T_new) of sequence b receive the new k
-// (rotated at its absolute position) and v, with pos_b = cache_seqlens[b] read
-// on the device. One workgroup per (new row, sequence). The lengths are
-// advanced by a second launch on the same stream, so every workgroup of the
-// first one has read the old positions before they change.
+// (optionally RMS-normalised, then rotated at its absolute position) and v,
+// with pos_b = cache_seqlens[b] read on the device. One workgroup per (new
+// row, sequence), one wave per KV head at a time: lane l holds head-dim
+// elements l + 64 m, so a row's norm is one wave reduction and each RoPE pair
+// (i, i + D/2) sits in one lane (D >= 128) or in lanes l, l ^ 32 (D = 64).
+// The lengths are advanced by a second launch on the same stream, so every
+// workgroup of the first one has read the old positions before they change.
 // ---------------------------------------------------------------------------
-template <typename T>
-__global__ void kv_append_kernel(const goda_kv_append_args a) {
+template <typename T, int D>
+__global__ void __launch_bounds__(256) kv_append_kernel(const goda_kv_append_args a) {
+  constexpr int M = D / 64;  // elements per lane
   const int t = blockIdx.x;
   const int b = blockIdx.y;
-  const int D = a.head_dim;
   const int pos = a.cache_seqlens[b] + t;
   if (pos < 0 || pos >= a.max_seqlen) return;
-  const T* kn = reinterpret_cast<const T*>(a.k_new) + (int64_t)b * a.kn_stride_b +
-                (int64_t)t * a.kn_stride_t;
-  const T* vn = reinterpret_cast<const T*>(a.v_new) + (int64_t)b * a.vn_stride_b +
-                (int64_t)t * a.vn_stride_t;
+  const int lane = threadIdx.x & 63;
+  const T* kn = reinterpret_cast<const T*>(a.k_new) + (int64_t)b * a.kn_stride_b + (int64_t)t * a.kn_stride_t;
+  const T* vn = reinterpret_cast<const T*>(a.v_new) + (int64_t)b * a.vn_stride_b + (int64_t)t * a.vn_stride_t;
   T* kc = reinterpret_cast<T*>(a.k_cache) + (int64_t)b * a.k_stride_b + (int64_t)pos * a.k_stride_t;
   T* vc = reinterpret_cast<T*>(a.v_cache) + (int64_t)b * a.v_stride_b + (int64_t)pos * a.v_stride_t;
-  const int half = D / 2;
-  for (int idx = threadIdx.x; idx < a.heads_kv * half; idx += blockDim.x) {
-    const int h = idx / half, i = idx % half;
-    const float x1 = Elem<T>::to_f32(kn[(int64_t)h * a.kn_stride_h + i]);
-    const float x2 = Elem<T>::to_f32(kn[(int64_t)h * a.kn_stride_h + i + half]);
-    float y1 = x1, y2 = x2;
-    if (a.rope_k) {
-      const int rp = pos + a.rope_k_offset;
-      const float cc = a.rope_cos[(int64_t)rp * half + i], ss = a.rope_sin[(int64_t)rp * half + i];
-      y1 = x1 * cc - x2 * ss;
-      y2 = x1 * ss + x2 * cc;
+  const int rp = pos + a.rope_k_offset;
+  for (int h = threadIdx.x >> 6; h < a.heads_kv; h += 4) {
+    float x[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) x[m] = Elem<T>::to_f32(kn[(int64_t)h * a.kn_stride_h + lane + 64 * m]);
+    if (a.k_norm_weight) {
+      float ss = 0.f;
+#pragma unroll
+      for (int m = 0; m < M; ++m) ss = fmaf(x[m], x[m], ss);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += shfl_xor_f(ss, o);
+      const float inv = rms_scale(ss, D, a.norm_eps);
+#pragma unroll
+      for (int m = 0; m < M; ++m) x[m] *= inv * (1.f + a.k_norm_weight[lane + 64 * m]);
     }
-    kc[(int64_t)h * a.k_stride_h + i] = Elem<T>::from_f32(y1);
-    kc[(int64_t)h * a.k_stride_h + i + half] = Elem<T>::from_f32(y2);
-    vc[(int64_t)h * a.v_stride_h + i] = vn[(int64_t)h * a.vn_stride_h + i];
-    vc[(int64_t)h * a.v_stride_h + i + half] = vn[(int64_t)h * a.vn_stride_h + i + half];
+    if (a.rope_k) {
+      if constexpr (M == 1) {
+        // pair (l, l + 32): lanes l < 32 hold x1, lanes l >= 32 hold x2
+        const float other = shfl_xor_f(x[0], 32);
+        const int f = lane & 31;
+        const float c = a.rope_cos[(int64_t)rp * (D / 2) + f], sn = a.rope_sin[(int64_t)rp * (D / 2) + f];
+        x[0] = lane < 32 ? x[0] * c - other * sn : other * sn + x[0] * c;
+      } else {
+#pragma unroll
+        for (int m = 0; m < M / 2; ++m) {
+          const int f = lane + 64 * m;
+          const float c = a.rope_cos[(int64_t)rp * (D / 2) + f], sn = a.rope_sin[(int64_t)rp * (D / 2) + f];
+          const float x1 = x[m], x2 = x[m + M / 2];
+          x[m] = x1 * c - x2 * sn;
+          x[m + M / 2] = x1 * sn + x2 * c;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      kc[(int64_t)h * a.k_stride_h + lane + 64 * m] = Elem<T>::from_f32(x[m]);
+      vc[(int64_t)h * a.v_stride_h + lane + 64 * m] = vn[(int64_t)h * a.vn_stride_h + lane + 64 * m];
+    }
   }
 }
 
@@ -635,7 +693,20 @@ __global__ void kv_bump_kernel(int32_t* seqlens, int n, int add) {
 template <typename T>
 hipError_t launch_append_t(const goda_kv_append_args& a, hipStream_t s) {
   if (a.seqlen_new > 0) {
-    kv_append_kernel<T><<<dim3(a.seqlen_new, a.batch), 256, 0, s>>>(a);
+    const dim3 grid(a.seqlen_new, a.batch);
+    switch (a.head_dim) {
+      case 64:
+        kv_append_kernel<T, 64><<<grid, 256, 0, s>>>(a);
+        break;
+      case 128:
+        kv_append_kernel<T, 128><<<grid, 256, 0, s>>>(a);
+        break;
+      case 256:
+        kv_append_kernel<T, 256><<<grid, 256, 0, s>>>(a);
+        break;
+      default:
+        return hipErrorNotSupported;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

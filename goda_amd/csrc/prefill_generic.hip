@@ -77,6 +77,19 @@ prefill_generic_kernel(const PrefillParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) q[4 * gi + j] = t4[j];
     }
+    if (a.q_norm_weight) {
+      // Fused QK-RMSNorm over the row held by the 4 threads of the row.
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < NPER; ++e) ss = fmaf(q[e], q[e], ss);
+      ss += shfl_xor_f(ss, 1);
+      ss += shfl_xor_f(ss, 2);
+      const float inv = rms_scale(ss, D, a.norm_eps);
+#pragma unroll
+      for (int gi = 0; gi < NGRP; ++gi)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[4 * gi + j] *= inv * (1.f + a.q_norm_weight[16 * gi + 4 * part + j]);
+    }
     if (a.rope_q) {
       const int pos = min(max(a.rope_q_offset + diag + i, 0), a.rope_len - 1);
       const float* cs = a.rope_cos + (int64_t)pos * (D / 2);
@@ -130,7 +143,7 @@ prefill_generic_kernel(const PrefillParams p) {
         load4<T>(krow + c4 + D / 2, k2);
         load4<T>(vrow + c4, v1);
         load4<T>(vrow + c4 + D / 2, v2);
-        if (a.rope_k) {
+        if (a.rope_k && !a.k_norm_weight) {  // with the norm: rotated after it
           const int pos = a.rope_k_offset + j;
           const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c4;
           const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c4;
@@ -148,6 +161,32 @@ prefill_generic_kernel(const PrefillParams p) {
         Ks[jr][c4 + D / 2 + e] = k2[e];
         Vs[jr][c4 + e] = v1[e];
         Vs[jr][c4 + D / 2 + e] = v2[e];
+      }
+    }
+    if (a.k_norm_weight) {
+      // Fused QK-RMSNorm of the staged key rows (staged unrotated on this
+      // path), then their rotation: 8 threads per row.
+      __syncthreads();
+      const int jr = tid >> 3, p8 = tid & 7;
+      float ss = 0.f;
+      for (int d = p8; d < D; d += 8) ss = fmaf(Ks[jr][d], Ks[jr][d], ss);
+      ss += shfl_xor_f(ss, 1);
+      ss += shfl_xor_f(ss, 2);
+      ss += shfl_xor_f(ss, 4);
+      const float inv = rms_scale(ss, D, a.norm_eps);
+      const int j = kv0 + jr;
+      const int pos = a.rope_k_offset + j;
+      for (int f = p8; f < D / 2; f += 8) {
+        float x1 = Ks[jr][f] * inv * (1.f + a.k_norm_weight[f]);
+        float x2 = Ks[jr][f + D / 2] * inv * (1.f + a.k_norm_weight[f + D / 2]);
+        if (a.rope_k && j < g.lk) {
+          const float c = a.rope_cos[(int64_t)pos * (D / 2) + f], sn = a.rope_sin[(int64_t)pos * (D / 2) + f];
+          const float y1 = x1 * c - x2 * sn;
+          x2 = x1 * sn + x2 * c;
+          x1 = y1;
+        }
+        Ks[jr][f] = x1;
+        Ks[jr][f + D / 2] = x2;
       }
     }
     __syncthreads();

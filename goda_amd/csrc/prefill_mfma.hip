@@ -118,9 +118,69 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
   // One row-major staging buffer, used for K then for V; +8 elements per row
   // keep the column reads of the transposes off a single bank.
   __shared__ __align__(16) T rows[BKV][D + 8];
+  __shared__ float inv_rms[BKV];
   const int tid = threadIdx.x;
   constexpr int HALF8 = D / 16;  // 8-element chunks per half row
 
+  if (a.k_norm_weight) {
+    // Fused QK-RMSNorm: raw rows staged first, then each row's scale, then
+    // normalisation and rotation in fp32 in place (one rounding).
+    for (int idx = tid; idx < BKV * (D / 8); idx += 256) {
+      const int r = idx / (D / 8);
+      const int c = (idx % (D / 8)) * 8;
+      const int row = kv0 + r;
+      v8 x = {};
+      if (row < g.lk) x = ld_vec<v8>(kbase + (g.k_row0 + row) * a.k_stride_t + c);
+      st_vec<v8>(&rows[r][c], x);
+    }
+    __syncthreads();
+    {
+      constexpr int TPN = 256 / BKV;  // threads per row
+      const int r = tid / TPN, part = tid % TPN;
+      float ss = 0.f;
+      for (int d = part; d < D; d += TPN) {
+        const float x = (float)rows[r][d];
+        ss = fmaf(x, x, ss);
+      }
+#pragma unroll
+      for (int o = 1; o < TPN; o <<= 1) ss += shfl_xor_f(ss, o);
+      if (part == 0) inv_rms[r] = rms_scale(ss, D, a.norm_eps);
+    }
+    __syncthreads();
+    for (int idx = tid; idx < BKV * HALF8; idx += 256) {
+      const int r = idx / HALF8;
+      const int c = (idx % HALF8) * 8;
+      const int row = kv0 + r;
+      const float inv = inv_rms[r];
+      v8 k1 = ld_vec<v8>(&rows[r][c]);
+      v8 k2 = ld_vec<v8>(&rows[r][c + D / 2]);
+      float x1[8], x2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x1[e] = (float)k1[e] * inv * (1.f + a.k_norm_weight[c + e]);
+        x2[e] = (float)k2[e] * inv * (1.f + a.k_norm_weight[c + D / 2 + e]);
+      }
+      if (a.rope_k && row < g.lk) {
+        const int pos = a.rope_k_offset + row;
+        const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
+        const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float y1 = x1[e] * cs[e] - x2[e] * sn[e];
+          const float y2 = x1[e] * sn[e] + x2[e] * cs[e];
+          x1[e] = y1;
+          x2[e] = y2;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        k1[e] = (T)x1[e];
+        k2[e] = (T)x2[e];
+      }
+      st_vec<v8>(&rows[r][c], k1);
+      st_vec<v8>(&rows[r][c + D / 2], k2);
+    }
+  } else {
   // K: coalesced row loads, rotation of the (i, i + D/2) pairs, staged.
   for (int idx = tid; idx < BKV * HALF8; idx += 256) {
     const int r = idx / HALF8;
@@ -149,6 +209,7 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
     }
     st_vec<v8>(&rows[r][c], k1);
     st_vec<v8>(&rows[r][c + D / 2], k2);
+  }
   }
   __syncthreads();
   // K' image: chunk (c, r) at c*BKV + r; consecutive threads write
@@ -272,24 +333,50 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         const T* qr = qbase + (g.q_row0 + qi) * a.q_stride_t;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = ld_vec<v8>(qr + 16 * ks + 8 * hi);
-        if (a.rope_q) {
-          const int pos = min(max(a.rope_q_offset + diag + qi, 0), a.rope_len - 1);
+        if (a.q_norm_weight || a.rope_q) {
+          // fp32 round trip: fused QK-RMSNorm, then RoPE, one rounding.
+          float xf[KS][8];
 #pragma unroll
-          for (int ks = 0; ks < KS / 2; ++ks) {
-            const int f0 = 16 * ks + 8 * hi;
-            const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + f0;
-            const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + f0;
-            const f32x4 c0 = ld_vec<f32x4>(cs), c1 = ld_vec<f32x4>(cs + 4);
-            const f32x4 s0 = ld_vec<f32x4>(sn), s1 = ld_vec<f32x4>(sn + 4);
+          for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float cc = e < 4 ? c0[e & 3] : c1[e & 3];
-              const float ss = e < 4 ? s0[e & 3] : s1[e & 3];
-              const float x1 = (float)qf[nt][ks][e], x2 = (float)qf[nt][ks + KS / 2][e];
-              qf[nt][ks][e] = (T)(x1 * cc - x2 * ss);
-              qf[nt][ks + KS / 2][e] = (T)(x1 * ss + x2 * cc);
+            for (int e = 0; e < 8; ++e) xf[ks][e] = (float)qf[nt][ks][e];
+          if (a.q_norm_weight) {
+            float ss = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) ss = fmaf(xf[ks][e], xf[ks][e], ss);
+            const float inv = rms_scale(half_sum(ss), D, a.norm_eps);  // lanes l, l^32 hold the row
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              const float* w = a.q_norm_weight + 16 * ks + 8 * hi;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) xf[ks][e] *= inv * (1.f + w[e]);
             }
           }
+          if (a.rope_q) {
+            const int pos = min(max(a.rope_q_offset + diag + qi, 0), a.rope_len - 1);
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks) {
+              const int f0 = 16 * ks + 8 * hi;
+              const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + f0;
+              const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + f0;
+              const f32x4 c0 = ld_vec<f32x4>(cs), c1 = ld_vec<f32x4>(cs + 4);
+              const f32x4 s0 = ld_vec<f32x4>(sn), s1 = ld_vec<f32x4>(sn + 4);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float cc = e < 4 ? c0[e & 3] : c1[e & 3];
+                const float ss = e < 4 ? s0[e & 3] : s1[e & 3];
+                const float x1 = xf[ks][e], x2 = xf[ks + KS / 2][e];
+                xf[ks][e] = x1 * cc - x2 * ss;
+                xf[ks + KS / 2][e] = x1 * ss + x2 * cc;
+              }
+            }
+          }
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[nt][ks][e] = (T)xf[ks][e];
         }
       } else {
 #pragma unroll

@@ -44,11 +44,14 @@ class KVCache:
         *,
         rope_cos: torch.Tensor | None = None,
         rope_sin: torch.Tensor | None = None,
+        k_norm_weight: torch.Tensor | None = None,
+        norm_eps: float = 1e-6,
     ) -> None:
         """Write k/v [B, T, Hkv, D] at rows cache_seqlens[b] .. +T-1 of each
         sequence b and advance cache_seqlens[:B] by T, all on the device. With
         RoPE tables, k is rotated at its absolute cache position on the way in
-        (goda caches post-RoPE keys, mint/nn/attn.py:60)."""
+        (goda caches post-RoPE keys, mint/nn/attn.py:60); with k_norm_weight it
+        is first RMS-normalised like goda's k_norm (mint/nn/attn.py:58)."""
         ops.kv_append(
             k,
             v,
@@ -58,6 +61,8 @@ class KVCache:
             rope_cos=rope_cos,
             rope_sin=rope_sin,
             rope_k=rope_cos is not None,
+            k_norm_weight=k_norm_weight,
+            norm_eps=norm_eps,
         )
 
     def update(self, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0) -> tuple[torch.Tensor, torch.Tensor]:

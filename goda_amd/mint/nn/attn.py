@@ -1,13 +1,15 @@
 """goda's attention layers (mint/nn/attn.py:10-145) on the HIP kernels.
 
 Same constructors and `forward(x, kv_cache, start_pos, base_attn_mask,
-doc_ids)`. The difference is where the positional encoding happens: a RoPE
-or ALiBi `pos_embeddings` from `goda_amd.mint.nn.pos` is fused into the
+doc_ids)`. The difference is where the per-head prologue happens: a RoPE or
+ALiBi `pos_embeddings` from `goda_amd.mint.nn.pos` is fused into the
 attention kernels (q and k are rotated while the kernels stage them; ALiBi is
 added to the scores) instead of running as separate elementwise passes, and
 ALiBi is actually applied (the reference asserts it away, mint/nn/attn.py:62).
-Any other `pos_embeddings` module is called as in the reference and must not
-return a bias.
+Without autograd (generation, evaluation) the QK-RMSNorm (mint/nn/attn.py:57-58)
+is fused too, so q and k reach the kernels straight from the projections;
+under autograd it stays a differentiable torch op. Any other `pos_embeddings`
+module is called as in the reference and must not return a bias.
 """
 
 from __future__ import annotations
@@ -75,14 +77,19 @@ class GroupedQueryAttention(nn.Module):
         q = self.wq(x).view(bsz, seqlen, self.n_heads, self.head_dim)
         k = self.wk(x).view(bsz, seqlen, self.n_kv_heads, self.head_dim)
         v = self.wv(x).view(bsz, seqlen, self.n_kv_heads, self.head_dim)
-        q = self.q_norm(q)
-        k = self.k_norm(k)
 
         fused: dict = {}
+        fusable = isinstance(self.pos_embeddings, (RoPE, ALiBiPositionalBias))
+        norms_plain = self.q_norm.shift is None and self.k_norm.shift is None and self.q_norm.eps == self.k_norm.eps
+        if fusable and norms_plain and not torch.is_grad_enabled():
+            fused["qk_norm"] = (self.q_norm.scale, self.k_norm.scale, self.q_norm.eps)
+        else:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
         if isinstance(self.pos_embeddings, RoPE):
-            fused = {"rope": (self.pos_embeddings.cos, self.pos_embeddings.sin), "start_pos": start_pos}
+            fused.update(rope=(self.pos_embeddings.cos, self.pos_embeddings.sin), start_pos=start_pos)
         elif isinstance(self.pos_embeddings, ALiBiPositionalBias):
-            fused = {"alibi_slopes": self.pos_embeddings.slopes}
+            fused["alibi_slopes"] = self.pos_embeddings.slopes
         else:
             q, k, attn_bias = self.pos_embeddings(q, k, start_pos=start_pos)
             if attn_bias is not None:

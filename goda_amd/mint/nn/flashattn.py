@@ -19,8 +19,12 @@ pretrain.py / sfttrain.py). The KV-cache path is inference only.
 
 Extra keyword arguments fuse the positional encoding into the kernels:
 `rope=(cos, sin)` fp32 tables with `start_pos` (q and k are then passed
-UNROTATED), or `alibi_slopes` [Hq]. There is no SDPA or CPU fallback:
-unsupported inputs (an arbitrary `base_attn_mask`, a right window) raise.
+UNROTATED), or `alibi_slopes` [Hq]; `qk_norm=(q_scale, k_scale, eps)` fuses
+goda's QK-RMSNorm (mint/nn/norm.py:17-27, weight 1 + scale, before RoPE) into
+the kernels' q/k loads when no gradient is needed (with autograd active it is
+applied as ordinary differentiable torch ops instead). There is no SDPA or
+CPU fallback: unsupported inputs (an arbitrary `base_attn_mask`, a right
+window) raise.
 """
 
 from __future__ import annotations
@@ -66,6 +70,7 @@ class FlashAttention(nn.Module):
         rope: tuple[torch.Tensor, torch.Tensor] | None = None,
         start_pos: int = 0,
         alibi_slopes: torch.Tensor | None = None,
+        qk_norm: tuple[torch.Tensor, torch.Tensor, float] | None = None,
     ) -> torch.Tensor:
         if base_attn_mask is not None:
             raise NotImplementedError(
@@ -74,16 +79,20 @@ class FlashAttention(nn.Module):
             )
         if window_size[1] != -1:
             raise NotImplementedError("goda_amd FlashAttention: only left windows (window_size[1] == -1)")
+        if qk_norm is not None and (doc_ids is not None or _needs_grad(q, k, *qk_norm[:2])):
+            # Differentiable (or pre-rotation for doc_ids packing): plain torch.
+            q, k = rms_norm(q, qk_norm[0], qk_norm[2]), rms_norm(k, qk_norm[1], qk_norm[2])
+            qk_norm = None
         if kv_cache is None:
             return self._attention(q, k, v, causal=causal, window_left=window_size[0], doc_ids=doc_ids,
-                                   rope=rope, start_pos=start_pos, alibi_slopes=alibi_slopes)
+                                   rope=rope, start_pos=start_pos, alibi_slopes=alibi_slopes, qk_norm=qk_norm)
         if doc_ids is not None:
             raise NotImplementedError("goda_amd FlashAttention: doc_ids with a KV cache")
         return self._attention_with_kvcache(q, k, v, kv_cache, causal=causal, window_left=window_size[0],
-                                            rope=rope, alibi_slopes=alibi_slopes)
+                                            rope=rope, alibi_slopes=alibi_slopes, qk_norm=qk_norm)
 
     # mint/nn/flashattn.py:87-172
-    def _attention(self, q, k, v, *, causal, window_left, doc_ids, rope, start_pos, alibi_slopes):
+    def _attention(self, q, k, v, *, causal, window_left, doc_ids, rope, start_pos, alibi_slopes, qk_norm):
         b, t, hq, d = q.shape
         hkv = k.shape[2]
         window_left = window_left if window_left >= 0 else -1
@@ -107,7 +116,7 @@ class FlashAttention(nn.Module):
                 max_seqlen_k=max_len,
             )
             return o.reshape(b, t, hq, d)
-        kw = {}
+        kw = _norm_kwargs(qk_norm, q=True, k=True)
         if rope is not None:
             kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True, rope_k=True,
                       rope_q_offset=start_pos, rope_k_offset=start_pos)
@@ -115,28 +124,49 @@ class FlashAttention(nn.Module):
                                           alibi_slopes=alibi_slopes, **kw)
 
     # mint/nn/flashattn.py:174-219
-    def _attention_with_kvcache(self, q, k, v, kv_cache: KVCache, *, causal, window_left, rope, alibi_slopes):
+    def _attention_with_kvcache(self, q, k, v, kv_cache: KVCache, *, causal, window_left, rope, alibi_slopes, qk_norm):
         b, tq = q.shape[0], q.shape[1]
         window_left = window_left if window_left >= 0 else -1
-        if rope is not None:
-            kv_cache.append(k, v, rope_cos=rope[0], rope_sin=rope[1])
-        else:
-            kv_cache.append(k, v)
+        kv_cache.append(k, v, **({} if rope is None else dict(rope_cos=rope[0], rope_sin=rope[1])),
+                        **_norm_kwargs(qk_norm, q=False, k=True))
         k_cache, v_cache, seqlens = kv_cache.get_cache_tensors()
         used = seqlens[:b]
         if tq == 1:
-            kw = {}
+            kw = _norm_kwargs(qk_norm, q=True, k=False)
             if rope is not None:
                 kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
             # One new token: the bottom-right causal mask admits every cached
             # key, so causal and non-causal coincide (mint/nn/flashattn.py:245-264).
             return ops.attention_decode(q, k_cache, v_cache, used, window_left=window_left,
                                         alibi_slopes=alibi_slopes, **kw)
-        kw = {}
+        kw = _norm_kwargs(qk_norm, q=True, k=False)
         if rope is not None:
             kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
         return ops.attention_prefill(q, k_cache[:b], v_cache[:b], causal=causal, window_left=window_left,
                                      alibi_slopes=alibi_slopes, seqused_k=used, **kw)
+
+
+def _needs_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
+def _norm_kwargs(qk_norm, *, q: bool, k: bool) -> dict:
+    if qk_norm is None:
+        return {}
+    kw = {"norm_eps": float(qk_norm[2])}
+    if q:
+        kw["q_norm_weight"] = qk_norm[0]
+    if k:
+        kw["k_norm_weight"] = qk_norm[1]
+    return kw
+
+
+def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
+    """goda's RMSNorm (mint/nn/norm.py:17-27) as torch ops: fp32
+    x * rsqrt(mean(x^2) + eps) * (1 + scale), cast back to x's dtype."""
+    x_f = x.float()
+    out = x_f * torch.rsqrt(x_f.pow(2).mean(dim=-1, keepdim=True) + eps) * (1.0 + scale.float())
+    return out.to(x.dtype)
 
 
 def _rotate(x: torch.Tensor, rope: tuple[torch.Tensor, torch.Tensor], start_pos: int) -> torch.Tensor:

@@ -58,7 +58,7 @@ def _i32_vec(name: str, t: torch.Tensor | None, n: int, device: torch.device) ->
 def _f32_vec(name: str, t: torch.Tensor | None, n: int, device: torch.device) -> torch.Tensor | None:
     if t is None:
         return None
-    t = t.reshape(-1)
+    t = t.detach().reshape(-1)
     if t.numel() != n:
         raise ValueError(f"goda_amd: {name} must have {n} elements")
     return t.to(device=device, dtype=torch.float32).contiguous()
@@ -151,6 +151,9 @@ def _prefill_args(
     rope_k: bool = False,
     rope_q_offset: int = 0,
     rope_k_offset: int = 0,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
+    norm_eps: float = 1e-6,
     cu_seqlens_q: torch.Tensor | None = None,
     cu_seqlens_k: torch.Tensor | None = None,
     max_seqlen_q: int | None = None,
@@ -254,8 +257,11 @@ def _prefill_args(
     a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
     a.rope_q, a.rope_k = int(bool(rope_q)), int(bool(rope_k))
     a.rope_q_offset, a.rope_k_offset = int(rope_q_offset), int(rope_k_offset)
+    qn = _f32_vec("q_norm_weight", q_norm_weight, d, dev)
+    kn = _f32_vec("k_norm_weight", k_norm_weight, d, dev)
+    a.q_norm_weight, a.k_norm_weight, a.norm_eps = _ptr(qn), _ptr(kn), float(norm_eps)
 
-    keep = (q, k, v, o, lse, slopes, cos, sin, cu_q, cu_k, used)
+    keep = (q, k, v, o, lse, slopes, cos, sin, cu_q, cu_k, used, qn, kn)
     return a, keep, o, lse
 
 
@@ -333,6 +339,8 @@ def plan_decode(
     rope_sin: torch.Tensor | None = None,
     rope_q: bool = False,
     rope_q_offset: int = 0,
+    q_norm_weight: torch.Tensor | None = None,
+    norm_eps: float = 1e-6,
     split_size: int = 0,
     cache_layout: str = "bthd",
     return_lse: bool = False,
@@ -402,6 +410,8 @@ def plan_decode(
     a.alibi_slopes = _ptr(slopes)
     a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
     a.rope_q, a.rope_q_offset = int(bool(rope_q)), int(rope_q_offset)
+    qn = _f32_vec("q_norm_weight", q_norm_weight, d, dev)
+    a.q_norm_weight, a.norm_eps = _ptr(qn), float(norm_eps)
 
     lib = _lib.load()
     need = lib.goda_attn_decode_workspace_size(ctypes.byref(a))
@@ -412,7 +422,7 @@ def plan_decode(
         ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
     ov = o.unsqueeze(1) if squeeze else o
-    keep = (q, k_cache, v_cache, seqlens, o, lse, ws, slopes, cos, sin)
+    keep = (q, k_cache, v_cache, seqlens, o, lse, ws, slopes, cos, sin, qn)
     return Launch("goda_attn_decode", a, keep, (ov, lse) if return_lse else ov)
 
 
@@ -427,10 +437,14 @@ def kv_append(
     rope_sin: torch.Tensor | None = None,
     rope_k: bool = False,
     rope_k_offset: int = 0,
+    k_norm_weight: torch.Tensor | None = None,
+    norm_eps: float = 1e-6,
 ) -> None:
     """Write k_new/v_new [B, Tn, Hkv, D] into caches [Bmax, Lmax, Hkv, D] at
     each sequence's own position cache_seqlens[b], then advance the lengths —
-    all on the device, with no host read of the lengths."""
+    all on the device, with no host read of the lengths. k rows are
+    optionally RMS-normalised (goda's RMSNorm with weight 1 + k_norm_weight)
+    and then rotated before they are stored."""
     for name, t in (("k_new", k_new), ("v_new", v_new), ("k_cache", k_cache), ("v_cache", v_cache)):
         _require_gpu(name, t)
         _require_last_contig(name, t)
@@ -458,5 +472,8 @@ def kv_append(
     a.cache_seqlens = cache_seqlens.data_ptr()
     a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
     a.rope_k, a.rope_k_offset = int(bool(rope_k)), int(rope_k_offset)
+    kn = _f32_vec("k_norm_weight", k_norm_weight, d, dev)
+    a.k_norm_weight, a.norm_eps = _ptr(kn), float(norm_eps)
     _lib.check(_lib.load().goda_attn_kv_append(ctypes.byref(a), _stream()))
+    del kn  # ordered after the launch by the caching allocator
 

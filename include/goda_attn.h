@@ -30,6 +30,10 @@
  *     supplied fp32 cos/sin tables [rope_len, head_dim/2]; query row i is
  *     rotated at position rope_q_offset + (Lk - Lq) + i, key row j at
  *     rope_k_offset + j;
+ *   - the optional fused QK-RMSNorm is goda's RMSNorm (mint/nn/norm.py:17-27)
+ *     as applied to q and k before RoPE (mint/nn/attn.py:57-60): a head row
+ *     x becomes x * rsqrt(mean(x^2) + norm_eps) * (1 + w) in fp32, with a
+ *     caller supplied fp32 weight w [head_dim] (the module's `scale`);
  *   - lse = ln(sum_j exp(score_ij)) over the scaled, biased, unmasked scores
  *     (kernels_/flash_attn_gqa/cuda.py:496-499). A row with no visible key
  *     produces o = 0 and lse = -inf.
@@ -46,7 +50,7 @@
 extern "C" {
 #endif
 
-#define GODA_ATTN_ABI_VERSION 2
+#define GODA_ATTN_ABI_VERSION 3
 
 /* element types */
 #define GODA_DTYPE_F32 0
@@ -99,7 +103,12 @@ typedef struct goda_prefill_args {
   int32_t rope_k;              /* rotate k rows */
   int32_t rope_q_offset;
   int32_t rope_k_offset;
-  int32_t reserved0;
+  float norm_eps;              /* epsilon of the fused RMSNorm (goda: 1e-6) */
+
+  /* Fused QK-RMSNorm weights, fp32 [head_dim] each, or NULL (no norm on
+   * that side). Forward only: goda_attn_prefill_bwd rejects them. */
+  const float* q_norm_weight;
+  const float* k_norm_weight;
 
   void* workspace;             /* size from goda_attn_prefill_workspace_size */
   int64_t workspace_bytes;
@@ -142,7 +151,8 @@ typedef struct goda_decode_args {
   int32_t rope_len;
   int32_t rope_q;
   int32_t rope_q_offset;
-  int32_t reserved1;
+  float norm_eps;
+  const float* q_norm_weight; /* fused RMSNorm of q before RoPE, fp32 [head_dim], or NULL */
 
   void* workspace;           /* size from goda_attn_decode_workspace_size */
   int64_t workspace_bytes;
@@ -174,7 +184,8 @@ typedef struct goda_kv_append_args {
   int32_t rope_len;
   int32_t rope_k;
   int32_t rope_k_offset;
-  int32_t reserved0;
+  float norm_eps;
+  const float* k_norm_weight; /* fused RMSNorm of new k rows before RoPE, fp32 [head_dim], or NULL */
 } goda_kv_append_args;
 
 /* Gradients for goda_attn_prefill_bwd. Every tensor uses the (b, t, h)

@@ -413,3 +413,13 @@ def attention_grads(
                       alibi_slopes=alibi_slopes, scale=scale, dtype=dtype)
         o.backward(d_o.to("cpu", dtype))
     return qs.grad, ks.grad, vs.grad
+
+
+def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """goda's RMSNorm (mint/nn/norm.py:17-27), as applied to every q and k head
+    row before RoPE (mint/nn/attn.py:57-60): in fp32,
+    x * rsqrt(mean(x^2, -1) + eps) * (1 + scale), cast back to x's dtype."""
+    x_f = x.float() if x.dtype != torch.float64 else x
+    var = x_f.pow(2).mean(dim=-1, keepdim=True)
+    out = x_f * torch.rsqrt(var + eps) * (1.0 + scale.to(x_f.dtype))
+    return out.to(x.dtype)

@@ -1,0 +1,141 @@
+"""Fused QK-RMSNorm + RoPE prologue (goda's q_norm / k_norm, mint/nn/attn.py:57-60,
+applied inside the kernels' q/k loads) against the CPU oracle: RMSNorm
+(mint/nn/norm.py:17-27) then RoPE then attention, in fp32."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from goda_amd import ops
+from goda_amd import workloads as wl
+from goda_amd.mint.kvcache import KVCache
+from goda_amd.mint.nn import FlashAttention, GroupedQueryAttention, RoPE
+from oracle import attention as ref
+from tests.helpers import TOL, max_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+EPS = 1e-6
+
+
+def _rand(shape, dtype, seed, std=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+def _prep(x, w, cos, sin, pos):
+    """Oracle prologue: fp32 RMSNorm, then RoPE at `pos` (None: no RoPE)."""
+    y = ref.rms_norm(x.float(), w.float(), EPS)
+    return y if cos is None else ref.apply_rope(y, cos, sin, pos)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("rope", [False, True])
+def test_prefill_fused_qk_norm(dtype, d, rope):
+    b, t, hq, hkv = 2, 75, 8, 2
+    q = _rand((b, t, hq, d), dtype, 1, std=2.0)
+    k = _rand((b, t, hkv, d), dtype, 2, std=2.0)
+    v = _rand((b, t, hkv, d), dtype, 3)
+    wq, wk = _rand((d,), torch.float32, 4, std=0.2), _rand((d,), torch.float32, 5, std=0.2)
+    kw, cos, sin = {}, None, None
+    if rope:
+        cos, sin = wl.rope_tables(t, d, 10000.0)
+        kw.update(rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_q=True, rope_k=True)
+    o = ops.attention_prefill(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, q_norm_weight=wq.to(DEV),
+                              k_norm_weight=wk.to(DEV), norm_eps=EPS, **kw)
+    pos = torch.arange(t)
+    o_ref = ref.attention(_prep(q, wq, cos, sin, pos), _prep(k, wk, cos, sin, pos), v.float(), causal=True)
+    assert max_err(o, o_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [128, 256])
+def test_decode_fused_q_norm(dtype, d):
+    lens = [1, 40, 300, 777]
+    b, hq, hkv, lmax = len(lens), 8, 2, 800
+    q = _rand((b, hq, d), dtype, 1, std=2.0)
+    kc = _rand((b, lmax, hkv, d), dtype, 2)
+    vc = _rand((b, lmax, hkv, d), dtype, 3)
+    wq = _rand((d,), torch.float32, 4, std=0.2)
+    cos, sin = wl.rope_tables(lmax, d, 10000.0)
+    seqlens = torch.tensor(lens, dtype=torch.int32)
+    o = ops.attention_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), seqlens.to(DEV), rope_cos=cos.to(DEV),
+                             rope_sin=sin.to(DEV), rope_q=True, q_norm_weight=wq.to(DEV), norm_eps=EPS)
+    qr = torch.stack([_prep(q[i][None, None], wq, cos, sin, torch.tensor([lens[i] - 1]))[0, 0] for i in range(b)])
+    o_ref, _ = ref.decode_attention(qr, kc.float(), vc.float(), seqlens)
+    assert max_err(o, o_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_kv_append_fused_k_norm(dtype, d):
+    b, lmax, hkv, tn = 3, 64, 3, 4
+    start = torch.tensor([0, 7, 50], dtype=torch.int32)
+    kc = torch.zeros(b, lmax, hkv, d, dtype=dtype, device=DEV)
+    vc = torch.zeros_like(kc)
+    kn, vn = _rand((b, tn, hkv, d), dtype, 1, std=2.0), _rand((b, tn, hkv, d), dtype, 2)
+    wk = _rand((d,), torch.float32, 3, std=0.2)
+    cos, sin = wl.rope_tables(lmax, d, 10000.0)
+    seqlens = start.clone().to(DEV)
+    ops.kv_append(kn.to(DEV), vn.to(DEV), kc, vc, seqlens, rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_k=True,
+                  k_norm_weight=wk.to(DEV), norm_eps=EPS)
+    torch.cuda.synchronize()
+    assert seqlens.cpu().tolist() == (start + tn).tolist()
+    for i in range(b):
+        p0 = int(start[i])
+        k_ref = _prep(kn[i][None], wk, cos, sin, torch.arange(p0, p0 + tn))[0]
+        assert max_err(kc[i, p0 : p0 + tn], k_ref) <= (1e-5 if dtype == torch.float32 else 2e-2)
+        assert max_err(vc[i, p0 : p0 + tn], vn[i]) == 0.0
+
+
+def test_backward_rejects_fused_norm():
+    q = _rand((1, 16, 2, 64), torch.bfloat16, 1).to(DEV)
+    k = q[:, :, :1].contiguous()
+    w = torch.zeros(64, device=DEV)
+    o, lse = ops.attention_prefill(q, k, k, causal=True, q_norm_weight=w, return_lse=True)
+    with pytest.raises(Exception, match="forward only"):
+        ops.attention_prefill_bwd(q, k, k, o, lse, torch.ones_like(o), causal=True, q_norm_weight=w)
+
+
+def test_generate_loop_with_fused_norm_matches_reference():
+    """Chunked prefill then token-by-token decode through the KV cache with
+    qk_norm and RoPE fused: equals the full causal attention over
+    norm -> rope'd q, k (the KV-cache invariant with goda's QK-norm)."""
+    b, t0, steps, hq, hkv, d, lmax = 2, 30, 4, 8, 2, 128, 64
+    total = t0 + steps
+    q, k, v = _rand((b, total, hq, d), torch.bfloat16, 1, 2.0), _rand((b, total, hkv, d), torch.bfloat16, 2, 2.0), _rand((b, total, hkv, d), torch.bfloat16, 3)
+    wq, wk = _rand((d,), torch.float32, 4, std=0.2), _rand((d,), torch.float32, 5, std=0.2)
+    cos, sin = wl.rope_tables(lmax, d, 10000.0)
+    rope = (cos.to(DEV), sin.to(DEV))
+    norm = (wq.to(DEV), wk.to(DEV), EPS)
+    cache = KVCache(max_batch_size=b, max_seq_len=lmax, n_kv_heads=hkv, head_dim=d, dtype=torch.bfloat16, device=DEV)
+    fa = FlashAttention()
+    outs = [fa(q[:, :t0].to(DEV), k[:, :t0].to(DEV), v[:, :t0].to(DEV), causal=True, kv_cache=cache, rope=rope, qk_norm=norm)]
+    for s in range(t0, total):
+        outs.append(fa(q[:, s : s + 1].to(DEV), k[:, s : s + 1].to(DEV), v[:, s : s + 1].to(DEV), causal=True,
+                       kv_cache=cache, rope=rope, qk_norm=norm))
+    o = torch.cat([x.cpu().float() for x in outs], dim=1)
+    pos = torch.arange(total)
+    o_ref = ref.attention(_prep(q, wq, cos, sin, pos), _prep(k, wk, cos, sin, pos), v.float(), causal=True)
+    assert max_err(o, o_ref) <= 2e-2
+
+
+def test_gqa_layer_inference_fuses_norm_and_matches_training_path():
+    """GroupedQueryAttention under no_grad (fused norm) equals the same layer
+    with autograd on (norm as torch ops), and the CPU reference."""
+    torch.manual_seed(3)
+    e, hq, hkv, d, t = 256, 4, 2, 128, 40
+    rope = RoPE(seq_len=64, head_dim=d, rope_base_theta=10000)
+    layer = GroupedQueryAttention(hq, hkv, d, e, rope, torch.float32).to(DEV)
+    with torch.no_grad():
+        for p_ in layer.parameters():
+            p_.normal_(0, 0.05)
+        layer.q_norm.scale.normal_(0, 0.2)
+        layer.k_norm.scale.normal_(0, 0.2)
+    x = (torch.randn(2, t, e) * 0.5).to(DEV)
+    with torch.no_grad():
+        y_fused = layer(x)
+    y_train = layer(x)  # autograd on: norm outside the kernel
+    assert max_err(y_fused, y_train.detach()) <= 1e-4 * max(1.0, y_train.abs().max().item())

@@ -410,3 +410,29 @@ def test_autograd_oracle_through_rope_matches_finite_differences():
     assert np.abs(dq.numpy() - fq).max() < 1e-5
     assert np.abs(dk.numpy() - fk).max() < 1e-5
     assert np.abs(dv.numpy() - fv).max() < 1e-7
+
+
+# ---------------------------------------------------------------------------
+# QK-RMSNorm
+# ---------------------------------------------------------------------------
+def test_rms_norm_matches_library_and_closed_form():
+    x = _rand((2, 5, 3, 16), 21)
+    scale = _rand((16,), 22) * 0.1
+    y = ref.rms_norm(x, scale, 1e-6)
+    # library routine: torch's rms_norm with weight (1 + scale)
+    assert torch.allclose(y, torch.nn.functional.rms_norm(x, (16,), weight=1.0 + scale, eps=1e-6), atol=1e-12)
+    # closed form: a constant row c maps to sign(c) * (1 + scale) (eps -> 0)
+    c = torch.full((16,), -3.0, dtype=F64)
+    assert torch.allclose(ref.rms_norm(c, scale, 0.0), -(1.0 + scale), atol=1e-12)
+    # zero-initialised scale (mint/nn/norm.py:13) gives unit RMS rows
+    y0 = ref.rms_norm(x, torch.zeros(16, dtype=F64), 0.0)
+    assert torch.allclose(y0.pow(2).mean(-1), torch.ones(2, 5, 3, dtype=F64), atol=1e-12)
+
+
+def test_planted_rms_norm_without_one_plus_is_caught():
+    x = _rand((4, 16), 23)
+    scale = _rand((16,), 24) * 0.1
+    wrong = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * scale  # drops the "1 +"
+    lib = torch.nn.functional.rms_norm(x, (16,), weight=1.0 + scale, eps=1e-6)
+    assert not torch.allclose(wrong, lib, atol=1e-3)
+    assert torch.allclose(ref.rms_norm(x, scale, 1e-6), lib, atol=1e-12)
