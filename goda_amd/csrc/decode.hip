@@ -37,7 +37,9 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kChunk = 16;              // keys per wave step
 constexpr float kRescaleThresh = 8.0f;  // log2 units
-constexpr int NBUF = 2;                 // 16-key chunks in flight per wave
+// 16-key chunks in flight per wave (depth of the register ring).
+template <int D>
+constexpr int kNbuf = 2;
 constexpr int kMinRange = 64;           // keys; ranges are multiples of this
 constexpr int kMaxGrid = 2048;          // persistent grid bound (sizes the workspace)
 
@@ -380,6 +382,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
 
   // Ring of NBUF register sets: chunk ch + (NBUF-1)*kWaves is in flight while
   // chunk ch is processed (the unrolled loop keeps every buffer index static).
+  constexpr int NBUF = kNbuf<D>;
   v8 kb[NBUF][KS], vb[NBUF][4][CPL];
 #pragma unroll
   for (int i = 0; i < NBUF - 1; ++i)
@@ -502,30 +505,35 @@ decode_splitk_kernel(const DecodeParams p) {
   }
 }
 
-// One workgroup per (unit, sequence): combines the partials of a unit that
-// spans several ranges, and writes o = 0, lse = -inf for a sequence with no
-// visible key. Units held whole by one range were written by the main kernel.
+// Combines the partials of a unit that spans several ranges, and writes
+// o = 0, lse = -inf for a sequence with no visible key; units held whole by
+// one range were written by the main kernel. Grid (head-dim blocks, unit,
+// sequence): each thread owns one (head, d) output element, and the partial
+// loads of a thread are issued four at a time.
+constexpr int kMergeThreads = 256;
+
 template <typename T, int D, int HMAX>
-__global__ void __launch_bounds__(256) merge_kernel(const DecodeParams p) {
+__global__ void __launch_bounds__(kMergeThreads) merge_kernel(const DecodeParams p) {
   const goda_decode_args& a = p.a;
   const int nhs = (p.group + HMAX - 1) / HMAX;
   const int U = a.heads_kv * nhs;
-  const int j = blockIdx.x;
-  const int b = blockIdx.y;
+  const int j = blockIdx.y;
+  const int b = blockIdx.z;
   const int hk = j / nhs, hs = j % nhs;
   const int hq0 = hk * p.group + hs * HMAX;
   const int nh = min(HMAX, p.group - hs * HMAX);
+  const int idx = blockIdx.x * kMergeThreads + threadIdx.x;
+  const int h = idx / D, d = idx % D;
   long long all, before;
   visible_sums(a, b, &all, &before);
+  if (h >= nh) return;
   int kbeg;
   const int n = visible(a, b, &kbeg);
-  T* obase = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_stride_b;
+  T* orow = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_stride_b + (int64_t)(hq0 + h) * a.o_stride_h;
+  float* lse_out = a.lse ? a.lse + (int64_t)b * a.lse_stride_b + hq0 + h : nullptr;
   if (n == 0) {
-    for (int idx = threadIdx.x; idx < nh * D; idx += 256) {
-      const int h = idx / D, d = idx % D;
-      obase[(int64_t)(hq0 + h) * a.o_stride_h + d] = (T)0.f;
-      if (a.lse && d == 0) a.lse[(int64_t)b * a.lse_stride_b + hq0 + h] = kNegInf;
-    }
+    orow[d] = (T)0.f;
+    if (lse_out && d == 0) *lse_out = kNegInf;
     return;
   }
   const int64_t total = (int64_t)U * all;
@@ -538,25 +546,21 @@ __global__ void __launch_bounds__(256) merge_kernel(const DecodeParams p) {
   // The unit is the last segment of range r0 (slot 1) unless it starts that
   // range (slot 0), and the first segment (slot 0) of every later range.
   const int64_t slot0 = 2 * r0 + (S == r0 * per ? 0 : 1);
-  for (int idx = threadIdx.x; idx < nh * D; idx += 256) {
-    const int h = idx / D, d = idx % D;
-    float M = kNegInf;
-    for (int64_t r = r0; r <= r1; ++r) {
-      const int64_t sl = r == r0 ? slot0 : 2 * r;
-      M = fmaxf(M, part_lse[sl * HMAX + h]);
-    }
-    const float Mu = (M == kNegInf) ? 0.f : M;
-    float wsum = 0.f, o = 0.f;
-    for (int64_t r = r0; r <= r1; ++r) {
-      const int64_t sl = r == r0 ? slot0 : 2 * r;
-      const float w = __expf(part_lse[sl * HMAX + h] - Mu);
-      wsum += w;
-      o = fmaf(w, part_o[(sl * HMAX + h) * D + d], o);
-    }
-    const int hq = hq0 + h;
-    obase[(int64_t)hq * a.o_stride_h + d] = (T)(wsum > 0.f ? o / wsum : 0.f);
-    if (a.lse && d == 0) a.lse[(int64_t)b * a.lse_stride_b + hq] = wsum > 0.f ? Mu + logf(wsum) : kNegInf;
+  auto slot = [&](int64_t r) { return r == r0 ? slot0 : 2 * r; };
+  float M = kNegInf;
+#pragma unroll 4
+  for (int64_t r = r0; r <= r1; ++r) M = fmaxf(M, part_lse[slot(r) * HMAX + h]);
+  const float Mu = (M == kNegInf) ? 0.f : M;
+  float wsum = 0.f, o = 0.f;
+#pragma unroll 4
+  for (int64_t r = r0; r <= r1; ++r) {
+    const int64_t sl = slot(r);
+    const float w = __expf(part_lse[sl * HMAX + h] - Mu);
+    wsum += w;
+    o = fmaf(w, part_o[(sl * HMAX + h) * D + d], o);
   }
+  orow[d] = (T)(wsum > 0.f ? o / wsum : 0.f);
+  if (lse_out && d == 0) *lse_out = wsum > 0.f ? Mu + logf(wsum) : kNegInf;
 }
 
 // Workgroups of `kernel` the device holds at once (cached per device).
@@ -592,7 +596,8 @@ hipError_t launch_hd(DecodeParams p, hipStream_t s) {
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if ((e = record_timing(a.timing_end, s)) != hipSuccess) return e;
   const int nhs = (p.group + HMAX - 1) / HMAX;
-  merge_kernel<T, D, HMAX><<<dim3(a.heads_kv * nhs, a.batch), 256, 0, s>>>(p);
+  const dim3 mgrid((HMAX * D + kMergeThreads - 1) / kMergeThreads, a.heads_kv * nhs, a.batch);
+  merge_kernel<T, D, HMAX><<<mgrid, kMergeThreads, 0, s>>>(p);
   return hipGetLastError();
 }
 
