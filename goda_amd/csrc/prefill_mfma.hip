@@ -414,6 +414,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   }
   const float c = p.scale_log2;
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
+  const float alibi_s1 = slope2, alibi_s2 = 2.f * slope2, alibi_s3 = 3.f * slope2, alibi_s8 = 8.f * slope2;
 
   // ---- tile ring ----------------------------------------------------------------
   // Lane chunk c of this wave's share sits at the same offset in the
@@ -462,19 +463,32 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int iabs = diag + wrow0 + 32 * nt + l32;
+        // ALiBi: slope * (kv - iabs). Registers come in groups of 4
+        // consecutive keys, groups 8 keys apart: a group base advanced by
+        // 8 slope per group, plus {0, 1, 2, 3} slope inside the group (four
+        // loop-invariant values instead of one per register).
+        float bg = ALIBI ? slope2 * (float)(kvb + 4 * hi - iabs) : 0.f;
+        // Visibility as a range of the register's key offset
+        // off = kv - (kvb + 4 hi), a compile-time constant per register:
+        // lo_lim <= off <= hi_lim (no per-register key index is formed).
+        const int rel = kvb + 4 * hi;
+        int hi_lim = g.lk - 1 - rel;
+        if (a.causal) hi_lim = min(hi_lim, iabs - rel);
+        const int lo_lim = use_window ? iabs - a.window_left - rel : 0;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int kv = kvb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
+            const int off = 32 * mt + 8 * (r >> 2) + (r & 3);
             float t = s[mt][nt][r];
-            if (ALIBI) t = fmaf(t, c, slope2 * (float)(kv - iabs));
-            if (need_mask) {
-              bool vis = kv < g.lk;
-              if (a.causal) vis = vis && kv <= iabs;
-              if (use_window) vis = vis && (iabs - kv <= a.window_left);
-              t = vis ? t : kNegInf;
+            if (ALIBI) {
+              if ((r & 3) == 0 && (mt | r) != 0) bg += alibi_s8;
+              t = fmaf(t, c, bg);
+              if ((r & 3) == 1) t += alibi_s1;
+              if ((r & 3) == 2) t += alibi_s2;
+              if ((r & 3) == 3) t += alibi_s3;
             }
+            if (need_mask) t = (off >= lo_lim && off <= hi_lim) ? t : kNegInf;
             s[mt][nt][r] = t;
           }
       }
