@@ -128,6 +128,38 @@ def bench_prefill(w, steps, warmup):
     }
 
 
+def bench_backward(w, steps, warmup):
+    """Backward of the prefill workload: dq, dk, dv from the forward's o and
+    lse (one forward first, untimed). Work = 2.5x the forward's FLOPs (the
+    five score-sized products of the FA2 backward: S, dP, dV, dQ, dK)."""
+    import torch
+
+    from goda_amd import ops
+    from goda_amd import workloads as wl
+
+    inp = wl.prefill_inputs(w, "cuda")
+    kw = {}
+    if "rope_cos" in inp:
+        kw.update(rope_cos=inp["rope_cos"], rope_sin=inp["rope_sin"], rope_q=True, rope_k=True)
+    if "alibi_slopes" in inp:
+        kw["alibi_slopes"] = inp["alibi_slopes"]
+    o, lse = ops.attention_prefill(inp["q"], inp["k"], inp["v"], causal=w.causal, return_lse=True, **kw)
+    g = torch.Generator(device="cuda").manual_seed(w.seed + 7)
+    d_o = torch.randn(o.shape, generator=g, device="cuda", dtype=torch.float32).to(o.dtype)
+    launch = ops.plan_prefill_bwd(inp["q"], inp["k"], inp["v"], o, lse, d_o, causal=w.causal, **kw)
+    ms, kms = _time_steps(launch, steps, warmup)
+    flops = 2.5 * wl.prefill_flops(w, inp.get("lengths"))
+    del launch, inp, o, lse, d_o
+    return {
+        "workload": w.name + "_backward",
+        "flops": flops,
+        "ms_per_step": ms,
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "kernel_ms": kms,
+        "kernel_tflops": flops / (kms * 1e-3) / 1e12,
+    }
+
+
 def bench_decode(w, steps, warmup):
     from goda_amd import ops
     from goda_amd import workloads as wl
@@ -257,7 +289,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "backward"], default=None)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -297,6 +329,10 @@ def main() -> int:
         d5 = bench_decode(wl.CFG5.decode, steps, warmup)
         out["cfg5"] = {"prefill": p5, "decode": d5}
         _log(f"  {out['cfg5']}")
+    if args.only in (None, "backward"):
+        _log("bench: cfg2 backward")
+        out["bwd"] = bench_backward(wl.CFG2, min(steps, 5), min(warmup, 2))
+        _log(f"  {out['bwd']}")
 
     cpu = None
     cpu_dec = None
@@ -393,6 +429,28 @@ def main() -> int:
             "decode_hbm_frac": round(d5["gbps"] / peak_bw, 4),
             "decode_ms": round(d5["ms_per_step"], 4),
         }
+    if "bwd" in out:
+        bw = out["bwd"]
+        line["backward"] = {
+            "workload": bw["workload"],
+            "value": round(bw["tflops"], 2),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(bw["ms_per_step"], 4),
+            "mfma_peak_frac": round(bw["tflops"] / peak_tf, 4),
+            "roofline": {
+                "bound": "mfma",
+                "kernel": "backward (dk/dv + dq kernels)",
+                "achieved": round(bw["kernel_tflops"], 2),
+                "peak": peak_tf,
+                "unit": "TFLOP/s",
+                "frac": round(bw["kernel_tflops"] / peak_tf, 4),
+                "kernel_ms": round(bw["kernel_ms"], 4),
+                "flops_per_launch": bw["flops"],
+            },
+        }
+        if "cfg2" not in out and "cfg4" not in out:
+            line.update(value=line["backward"]["value"], unit="TFLOP/s", ms_per_step=line["backward"]["ms_per_step"],
+                        dtype="bf16", config={"workload": bw["workload"]}, roofline=line["backward"]["roofline"])
     print(json.dumps(line), flush=True)
     return 0
 

@@ -86,21 +86,26 @@ class Launch:
     of two recorded torch.cuda.Event(enable_timing=True)) that the library
     records right around its main kernel."""
 
-    def __init__(self, fn_name: str, args, keep: tuple, result):
+    def __init__(self, fn_name: str, args, keep: tuple, result, grads=None):
         self._fn = getattr(_lib.load(), fn_name)
         self.args = args
+        self.grads = grads  # the backward's second struct (it carries the timing events)
         self._keep = keep
         self.result = result
 
     def __call__(self, timing: tuple[int, int] | None = None):
         a = self.args
+        t = self.grads if self.grads is not None else a
         if timing is not None:
-            a.timing_begin, a.timing_end = timing
+            t.timing_begin, t.timing_end = timing
         try:
-            _lib.check(self._fn(ctypes.byref(a), _stream()))
+            if self.grads is not None:
+                _lib.check(self._fn(ctypes.byref(a), ctypes.byref(self.grads), _stream()))
+            else:
+                _lib.check(self._fn(ctypes.byref(a), _stream()))
         finally:
             if timing is not None:
-                a.timing_begin = a.timing_end = None
+                t.timing_begin = t.timing_end = None
         return self.result
 
 
@@ -265,7 +270,17 @@ def _prefill_args(
     return a, keep, o, lse
 
 
-def attention_prefill_bwd(
+def attention_prefill_bwd(q, k, v, o, lse, d_o, **kwargs):
+    """Gradients (dq, dk, dv) of `attention_prefill` through
+    `goda_attn_prefill_bwd`, from the forward's o and lse and the upstream
+    gradient d_o. Takes the forward's own keyword arguments (causal, window,
+    ALiBi, RoPE, varlen, seqused_k, scale), so the scores are recomputed
+    exactly as the forward computed them. dk/dv have Hkv heads (summed over
+    each KV head's query group) and are zero for keys past seqused_k."""
+    return plan_prefill_bwd(q, k, v, o, lse, d_o, **kwargs)()
+
+
+def plan_prefill_bwd(
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
@@ -274,12 +289,8 @@ def attention_prefill_bwd(
     d_o: torch.Tensor,
     **kwargs,
 ):
-    """Gradients (dq, dk, dv) of `attention_prefill` through
-    `goda_attn_prefill_bwd`, from the forward's o and lse and the upstream
-    gradient d_o. Takes the forward's own keyword arguments (causal, window,
-    ALiBi, RoPE, varlen, seqused_k, scale), so the scores are recomputed
-    exactly as the forward computed them. dk/dv have Hkv heads (summed over
-    each KV head's query group) and are zero for keys past seqused_k."""
+    """Validate and allocate once for `goda_attn_prefill_bwd`; returns the
+    `Launch` whose result is (dq, dk, dv)."""
     kwargs.pop("return_lse", None)
     kwargs.pop("out", None)
     a, keep, o, lse = _prefill_args(q, k, v, out=o, lse_in=lse, **kwargs)
@@ -315,9 +326,7 @@ def attention_prefill_bwd(
     if need > 0:
         ws = torch.empty(int(need), dtype=torch.uint8, device=q.device)
         g.workspace, g.workspace_bytes = ws.data_ptr(), int(need)
-    _lib.check(lib.goda_attn_prefill_bwd(ctypes.byref(a), ctypes.byref(g), _stream()))
-    del keep, ws  # the caching allocator orders reuse after this stream's work
-    return dq, dk, dv
+    return Launch("goda_attn_prefill_bwd", a, keep + (d_o, dq, dk, dv, ws), (dq, dk, dv), grads=g)
 
 
 def attention_decode(*args, **kwargs):
