@@ -6,7 +6,8 @@
 // This file holds the row-statistics pre-pass and the generic kernels: fp32
 // arithmetic on the vector ALUs for every dtype and head_dim in {64, 128,
 // 256} (the fp32 training path; goda's default model dtype is fp32,
-// mint/nn/models.py:23). Three launches:
+// mint/nn/models.py:23); bf16/fp16 with head_dim 64 or 128 run on the matrix
+// cores instead (backward_mfma.hip). Three launches:
 //   1. bwd_delta_kernel   delta[hq][row] = sum_d dO * O (fp32 workspace);
 //   2. bwd_dkv_kernel     one workgroup per (key block, KV head, sequence):
 //                         keys stay in registers, query rows of every head of
@@ -441,10 +442,12 @@ hipError_t launch_generic_t(const BwdParams& p, hipStream_t s) {
 }  // namespace
 
 int64_t prefill_bwd_workspace_bytes(const goda_prefill_args& a) {
+  if (prefill_bwd_mfma_supported(a)) return prefill_bwd_mfma_workspace_bytes(a);
   return (int64_t)a.heads_q * a.batch * a.seqlen_q * (int64_t)sizeof(float);
 }
 
 hipError_t launch_prefill_bwd(const BwdParams& p, hipStream_t s) {
+  if (prefill_bwd_mfma_supported(p.a)) return launch_prefill_bwd_mfma(p, s);
   switch (p.a.dtype) {
     case GODA_DTYPE_F32:
       return launch_generic_t<float>(p, s);

@@ -1,0 +1,712 @@
+// Backward of prefill attention on gfx950 matrix cores: bf16 / fp16 operands,
+// fp32 accumulation, head_dim 64 or 128 (others take the generic kernels).
+// Same quantities as kernels_/flash_attn_gqa/cuda.py:6-246:
+//   P = exp(scale q k^T + bias - lse), dV = P^T dO, dP = dO V^T,
+//   dS = P * (dP - delta) with delta = rowsum(dO * O),
+//   dQ = scale dS K, dK = scale dS^T Q.
+//
+// Four launches:
+//   1. pack_q_bwd_kernel: per (32-row query tile, query head, sequence),
+//      the operand images of rotated q and of dO, both row-major
+//      ("chunk-column-major" [D/8][32] 16-byte chunks, the A operand of a
+//      product over head_dim) and transposed ([32/8][D] chunks with the rows
+//      of each 16-row group in kPermKey order, the A operand of a product
+//      over rows), plus the row statistics lse*log2(e) and delta.
+//   2. pack_kv_bwd_kernel: per (64-key tile, KV head, sequence), the
+//      row-major images of rotated k and of v and the transposed image of k.
+//   3. bwd_dkv_mfma_kernel: one workgroup of 4 waves per 128 keys of a KV
+//      head; each wave pins the k and v operands of its 32 keys in registers
+//      and walks the query tiles of every head of the group (GQA reduction in
+//      the accumulators, no atomics), the tiles moving through a two-stage
+//      LDS ring:
+//        S    [rows][keys] = Q K^T        A = Q image,   B = k (registers)
+//        dV^T [d][keys]   += dO^T P        A = dO^T image, B = P (packed S)
+//        dP   [rows][keys] = dO V^T        A = dO image,  B = v (registers)
+//        dK^T [d][keys]   += Q^T dS        A = Q^T image, B = dS (packed)
+//   4. bwd_dq_mfma_kernel: one workgroup of 4 waves per (query tile, head
+//      slice); each wave pins the q and dO operands of its 32 rows and walks
+//      the key tiles:
+//        S^T  [keys][rows] = K Q^T         A = k image,   B = q (registers)
+//        dP^T [keys][rows] = V dO^T        A = v image,   B = dO (registers)
+//        dQ^T [d][rows]   += K^T dS^T      A = K^T image, B = dS^T (packed)
+// A packed accumulator becomes a B operand directly because the transposed
+// images hold their rows / keys in the accumulator's register order
+// (kPermKey). With the log-sum-exp known there is no online softmax.
+
+#include "common.h"
+#include "launch.h"
+#include "mfma_common.h"
+
+namespace goda {
+namespace {
+
+constexpr int kQRows = 32;  // rows per query tile
+constexpr int kBKV = 64;    // keys per key tile
+constexpr int kWaves = 4;
+
+template <int D>
+struct QImg {
+  static constexpr int CH = D / 8 * kQRows;  // 16-byte chunks of one image
+  static constexpr int QA = 0, GA = CH, QT = 2 * CH, GT = 3 * CH;
+  static constexpr int STAT = 4 * CH;        // lse2[32] then delta[32]: 16 chunks
+  static constexpr int CHUNKS = 4 * CH + 16;
+  static constexpr int64_t BYTES = (int64_t)CHUNKS * 16;
+};
+
+template <int D>
+struct KVImg {
+  static constexpr int CH = D / 8 * kBKV;
+  static constexpr int KA = 0, VA = CH, KT = 2 * CH;
+  static constexpr int CHUNKS = 3 * CH;
+  static constexpr int64_t BYTES = (int64_t)CHUNKS * 16;
+};
+
+__device__ __forceinline__ int64_t q_tile_index(int b, int qt, int hq, int ntq, int heads_q) {
+  return ((int64_t)b * ntq + qt) * heads_q + hq;
+}
+__device__ __forceinline__ int64_t kv_tile_index(int b, int j, int hk, int ntk, int heads_kv) {
+  return ((int64_t)b * ntk + j) * heads_kv + hk;
+}
+
+template <typename T>
+__device__ __forceinline__ const T* grow(const void* base, int64_t sb, int64_t st, int64_t sh, bool varlen, int b,
+                                         int64_t row, int h) {
+  return reinterpret_cast<const T*>(base) + (varlen ? 0 : (int64_t)b * sb) + row * st + (int64_t)h * sh;
+}
+
+// ---------------------------------------------------------------------------
+// 1. query-side images
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
+  typedef typename Vec<T>::v8 v8;
+  typedef QImg<D> QI;
+  const goda_prefill_args& a = p.a;
+  const int qt = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  const int i0 = qt * kQRows;
+  if (i0 >= g.lq) return;
+  const bool varlen = a.cu_seqlens_q != nullptr;
+  const int diag = g.lk - g.lq;
+  __shared__ __align__(16) T qrows[kQRows][D + 8];
+  __shared__ __align__(16) T grows[kQRows][D + 8];
+  const int tid = threadIdx.x;
+  constexpr int HALF8 = D / 16;
+
+  // rotated q and dO rows (zero past the sequence)
+  for (int idx = tid; idx < kQRows * HALF8; idx += 256) {
+    const int r = idx / HALF8;
+    const int c = (idx % HALF8) * 8;
+    const int i = i0 + r;
+    v8 q1 = {}, q2 = {}, g1 = {}, g2 = {};
+    if (i < g.lq) {
+      const T* qr = grow<T>(a.q, a.q_stride_b, a.q_stride_t, a.q_stride_h, varlen, b, g.q_row0 + i, hq);
+      const T* gr = grow<T>(p.g.d_o, p.g.do_stride_b, p.g.do_stride_t, p.g.do_stride_h, varlen, b, g.q_row0 + i, hq);
+      q1 = ld_vec<v8>(qr + c);
+      q2 = ld_vec<v8>(qr + c + D / 2);
+      g1 = ld_vec<v8>(gr + c);
+      g2 = ld_vec<v8>(gr + c + D / 2);
+      if (a.rope_q) {
+        const int pos = min(max(a.rope_q_offset + diag + i, 0), a.rope_len - 1);
+        const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
+        const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x1 = (float)q1[e], x2 = (float)q2[e];
+          q1[e] = (T)(x1 * cs[e] - x2 * sn[e]);
+          q2[e] = (T)(x1 * sn[e] + x2 * cs[e]);
+        }
+      }
+    }
+    st_vec<v8>(&qrows[r][c], q1);
+    st_vec<v8>(&qrows[r][c + D / 2], q2);
+    st_vec<v8>(&grows[r][c], g1);
+    st_vec<v8>(&grows[r][c + D / 2], g2);
+  }
+  __syncthreads();
+
+  v8* img = reinterpret_cast<v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
+  // row-major images: chunk (c, r) at c*32 + r
+  for (int idx = tid; idx < QI::CH; idx += 256) {
+    const int c = idx / kQRows, r = idx % kQRows;
+    img[QI::QA + idx] = ld_vec<v8>(&qrows[r][8 * c]);
+    img[QI::GA + idx] = ld_vec<v8>(&grows[r][8 * c]);
+  }
+  // transposed images: chunk (kc, d) at kc*D + d holds rows
+  // 16*(kc/2) + kPermKey(8*(kc%2) + e)
+  for (int idx = tid; idx < QI::CH; idx += 256) {
+    const int kc = idx / D, d = idx % D;
+    const int r0 = 16 * (kc / 2);
+    v8 tq, tg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int r = r0 + kPermKey(8 * (kc % 2) + e);
+      tq[e] = qrows[r][d];
+      tg[e] = grows[r][d];
+    }
+    img[QI::QT + idx] = tq;
+    img[QI::GT + idx] = tg;
+  }
+  // row statistics: 8 threads per row
+  {
+    const int r = tid >> 3, part = tid & 7;
+    const int i = i0 + r;
+    float dl = 0.f;
+    if (i < g.lq) {
+      const T* orow = grow<T>(a.o, a.o_stride_b, a.o_stride_t, a.o_stride_h, varlen, b, g.q_row0 + i, hq);
+      for (int d = part; d < D; d += 8) dl = fmaf((float)orow[d], (float)grows[r][d], dl);
+    }
+    dl += shfl_xor_f(dl, 1);
+    dl += shfl_xor_f(dl, 2);
+    dl += shfl_xor_f(dl, 4);
+    if (part == 0) {
+      float l2 = kNegInf;
+      if (i < g.lq) {
+        const int64_t li = a.cu_seqlens_q ? (int64_t)hq * a.lse_stride_h + g.q_row0 + i
+                                          : (int64_t)b * a.lse_stride_b + (int64_t)hq * a.lse_stride_h + i;
+        l2 = a.lse[li] * kLog2e;
+      }
+      float* st = reinterpret_cast<float*>(img + QI::STAT);
+      st[r] = l2;
+      st[kQRows + r] = dl;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. key-side images
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
+  typedef typename Vec<T>::v8 v8;
+  typedef KVImg<D> KI;
+  const goda_prefill_args& a = p.a;
+  const int j = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  const int kv0 = j * kBKV;
+  if (kv0 >= g.lk) return;
+  const bool varlen = a.cu_seqlens_k != nullptr;
+  __shared__ __align__(16) T krows[kBKV][D + 8];
+  __shared__ __align__(16) T vrows[kBKV][D + 8];
+  const int tid = threadIdx.x;
+  constexpr int HALF8 = D / 16;
+  for (int idx = tid; idx < kBKV * HALF8; idx += 256) {
+    const int r = idx / HALF8;
+    const int c = (idx % HALF8) * 8;
+    const int row = kv0 + r;
+    v8 k1 = {}, k2 = {}, v1 = {}, v2 = {};
+    if (row < g.lk) {
+      const T* kr = grow<T>(a.k, a.k_stride_b, a.k_stride_t, a.k_stride_h, varlen, b, g.k_row0 + row, hk);
+      const T* vr = grow<T>(a.v, a.v_stride_b, a.v_stride_t, a.v_stride_h, varlen, b, g.k_row0 + row, hk);
+      k1 = ld_vec<v8>(kr + c);
+      k2 = ld_vec<v8>(kr + c + D / 2);
+      v1 = ld_vec<v8>(vr + c);
+      v2 = ld_vec<v8>(vr + c + D / 2);
+      if (a.rope_k) {
+        const int pos = a.rope_k_offset + row;
+        const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
+        const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x1 = (float)k1[e], x2 = (float)k2[e];
+          k1[e] = (T)(x1 * cs[e] - x2 * sn[e]);
+          k2[e] = (T)(x1 * sn[e] + x2 * cs[e]);
+        }
+      }
+    }
+    st_vec<v8>(&krows[r][c], k1);
+    st_vec<v8>(&krows[r][c + D / 2], k2);
+    st_vec<v8>(&vrows[r][c], v1);
+    st_vec<v8>(&vrows[r][c + D / 2], v2);
+  }
+  __syncthreads();
+  v8* img = reinterpret_cast<v8*>(p.kvimg + kv_tile_index(b, j, hk, p.ntk, a.heads_kv) * KI::BYTES);
+  for (int idx = tid; idx < KI::CH; idx += 256) {
+    const int c = idx / kBKV, r = idx % kBKV;
+    img[KI::KA + idx] = ld_vec<v8>(&krows[r][8 * c]);
+    img[KI::VA + idx] = ld_vec<v8>(&vrows[r][8 * c]);
+  }
+  for (int idx = tid; idx < KI::CH; idx += 256) {
+    const int kc = idx / D, d = idx % D;
+    const int r0 = 16 * (kc / 2);
+    v8 t;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = krows[r0 + kPermKey(8 * (kc % 2) + e)][d];
+    img[KI::KT + idx] = t;
+  }
+}
+
+// Packs accumulator registers 8g..8g+7 of a 32x32 tile into an operand.
+template <typename V, typename T>
+__device__ __forceinline__ V pack8(const float* x) {
+  V v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (T)x[e];
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// 3. dk, dv
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool ALIBI>
+__global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdParams p) {
+  typedef typename Vec<T>::v8 v8;
+  typedef typename Vec<T>::v4 v4;
+  typedef QImg<D> QI;
+  typedef KVImg<D> KI;
+  constexpr int KS = D / 16;  // k-steps over head_dim
+  constexpr int MD = D / 32;  // 32-wide head_dim tiles of dK^T / dV^T
+  constexpr int LOADS = 4 * QI::CH / (kWaves * 64);
+  static_assert(4 * QI::CH % (kWaves * 64) == 0, "tile must split over the waves");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const goda_prefill_args& a = p.a;
+  const int b = blockIdx.z, hk = blockIdx.y;
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  const bool varlen = a.cu_seqlens_k != nullptr;
+  const int kend = varlen ? g.lk : a.seqlen_k;  // rows this launch writes
+  const int kv0 = blockIdx.x * (kWaves * 32);
+  if (kv0 >= kend) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int kw0 = kv0 + 32 * wave;
+  const int key = kw0 + l32;
+  const int diag = g.lk - g.lq;
+  const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
+
+  // B operands of this wave's 32 keys: k (rotated) and v rows, from the images.
+  v8 kf[KS], vf[KS];
+  if (kw0 < g.lk) {
+    const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
+    const int kin = kw0 % kBKV + l32;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + kin];
+      vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + kin];
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = vf[ks] = v8{};
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    asm volatile("" : "+v"(kf[ks]));
+    asm volatile("" : "+v"(vf[ks]));
+  }
+
+  f32x16 dk[MD], dv[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dk[md] = dv[md] = f32x16{};
+
+  // Query tiles that can see a key of this workgroup.
+  const int kv_last = min(kv0 + kWaves * 32, g.lk) - 1;
+  int i_lo = 0, i_hi = g.lq;
+  if (a.causal) i_lo = max(0, kv0 - diag);
+  if (use_window) i_hi = min(g.lq, kv_last + a.window_left - diag + 1);
+  if (kv0 >= g.lk) i_hi = i_lo;
+  const int qt_lo = i_lo / kQRows;
+  const int nq = i_hi > i_lo ? (i_hi - 1) / kQRows + 1 - qt_lo : 0;
+  const int n = p.group * nq;
+
+  // two-stage ring of query tiles: the main images (LOADS chunks per lane)
+  // plus the 16 statistics chunks (lanes 0..15 of wave 0)
+  v8 stg[LOADS];
+  v8 stg_stat;
+  auto tile_src = [&](int it) {
+    const int hq = hk * p.group + it / nq;
+    const int qt = qt_lo + it % nq;
+    return reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
+  };
+  auto tile_load = [&](int it) {
+    const v8* src = tile_src(it);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) stg[i] = src[tid + i * kWaves * 64];
+    if (tid < 16) stg_stat = src[QI::STAT + tid];
+  };
+  auto tile_store = [&](int it) {
+    v8* dst = reinterpret_cast<v8*>(smem + (it % 2) * QI::BYTES);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) dst[tid + i * kWaves * 64] = stg[i];
+    if (tid < 16) dst[QI::STAT + tid] = stg_stat;
+  };
+
+  const float c = p.scale_log2;
+  auto compute = [&](int it) {
+    const int hq = hk * p.group + it / nq;
+    const int q0 = (qt_lo + it % nq) * kQRows;
+    const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
+    const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
+    const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
+
+    // S[rows][keys]
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
+    // statistics of this lane's 16 rows: 8 (r/4) + 4 hi + r%4
+    f32x4 l2[4], dl[4];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      l2[gq] = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
+      dl[gq] = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+    }
+    // Visibility as a range of the register's row offset off = row - (q0 + 4 hi):
+    // causal key <= diag + row, window diag + row - key <= W, row < lq, key < lk.
+    const int rel = q0 + 4 * hi;
+    int lo_lim = -1, hi_lim = g.lq - 1 - rel;
+    if (a.causal) lo_lim = key - diag - rel;
+    if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
+    const bool key_ok = key < g.lk;
+    const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27 || kw0 + 31 >= g.lk;
+    // bias slope * (key - diag - row) = base - slope * off
+    const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
+    float pr[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int off = 8 * (r >> 2) + (r & 3);
+      float t = s[r] * c;
+      if (ALIBI) t += base - slope2 * (float)off;
+      float pv = fast_exp2(t - l2[r >> 2][r & 3]);
+      if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+      pr[r] = pv;
+    }
+    // dV^T += dO^T P
+    v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
+#pragma unroll
+    for (int md = 0; md < MD; ++md) {
+      dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
+      dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
+    }
+    // dP[rows][keys] = dO V^T
+    f32x16 dp = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ds[r] = pr[r] * (dp[r] - dl[r >> 2][r & 3]);
+    v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
+    // dK^T += Q^T dS
+#pragma unroll
+    for (int md = 0; md < MD; ++md) {
+      dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
+      dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
+    }
+  };
+
+  if (n > 0) {
+    tile_load(0);
+    tile_store(0);
+  }
+  ring_barrier();
+  for (int it = 0; it < n; ++it) {
+    if (it + 1 < n) tile_load(it + 1);
+    compute(it);
+    if (it + 1 < n) tile_store(it + 1);
+    ring_barrier();
+  }
+
+  // ---- epilogue: lane l32 owns key row `key`; register (md, r) is head-dim
+  // 32 md + 8 (r/4) + 4 hi + r%4.
+  if (key >= kend) return;
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dk[md] *= a.softmax_scale;
+  if (a.rope_k && key < g.lk) {
+    // transpose of the rotation: pairs (d, d + D/2) are blocks md, md + MD/2
+    const int pos = a.rope_k_offset + key;
+#pragma unroll
+    for (int md = 0; md < MD / 2; ++md)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
+        const float x1 = dk[md][r], x2 = dk[md + MD / 2][r];
+        dk[md][r] = x1 * cs + x2 * sn;
+        dk[md + MD / 2][r] = x2 * cs - x1 * sn;
+      }
+  }
+  T* dkrow = reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
+             (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h;
+  T* dvrow = reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
+             (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
+#pragma unroll
+  for (int md = 0; md < MD; ++md)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = 32 * md + 8 * gq + 4 * hi;
+      const v4 kv4 = {(T)dk[md][4 * gq], (T)dk[md][4 * gq + 1], (T)dk[md][4 * gq + 2], (T)dk[md][4 * gq + 3]};
+      const v4 vv4 = {(T)dv[md][4 * gq], (T)dv[md][4 * gq + 1], (T)dv[md][4 * gq + 2], (T)dv[md][4 * gq + 3]};
+      st_vec<v4>(dkrow + d0, kv4);
+      st_vec<v4>(dvrow + d0, vv4);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 4. dq
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool ALIBI>
+__global__ void __launch_bounds__(kWaves * 64, 1) bwd_dq_mfma_kernel(const BwdParams p) {
+  typedef typename Vec<T>::v8 v8;
+  typedef typename Vec<T>::v4 v4;
+  typedef QImg<D> QI;
+  typedef KVImg<D> KI;
+  constexpr int KS = D / 16;
+  constexpr int MD = D / 32;
+  constexpr int MT = kBKV / 32;   // 32-key blocks of S^T
+  constexpr int KS2 = kBKV / 16;  // k-steps of dQ^T over keys
+  constexpr int LOADS = KI::CHUNKS / (kWaves * 64);
+  static_assert(KI::CHUNKS % (kWaves * 64) == 0, "tile must split over the waves");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const goda_prefill_args& a = p.a;
+  const int hg = p.heads_per_wg;
+  const int nslices = p.group / hg;
+  const int qb_rows = (kWaves / hg) * 32;
+  const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
+  const int lin = blockIdx.x;
+  const int pair = lin / nqt;
+  const int qt = nqt - 1 - (lin % nqt);  // heavy causal tiles first
+  const int b = pair / (a.heads_kv * nslices);
+  const int rem = pair % (a.heads_kv * nslices);
+  const int hk = rem / nslices;
+  const int sl = rem % nslices;
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  const int qr0 = qt * qb_rows;
+  if (qr0 >= g.lq) return;
+  const bool varlen = a.cu_seqlens_q != nullptr;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int hq = hk * p.group + sl * hg + (wave % hg);
+  const int wrow0 = qr0 + (wave / hg) * 32;  // a 32-row query tile of the images
+  const int diag = g.lk - g.lq;
+  const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
+  const int i = wrow0 + l32;
+  const int iabs = diag + i;
+
+  // B operands of this wave's 32 rows: q (rotated) and dO, plus statistics.
+  v8 qf[KS], gf[KS];
+  float l2 = kNegInf, dl = 0.f;
+  if (wrow0 < g.lq) {
+    const v8* img = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, wrow0 / kQRows, hq, p.ntq, a.heads_q) * QI::BYTES);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = img[QI::QA + (2 * ks + hi) * kQRows + l32];
+      gf[ks] = img[QI::GA + (2 * ks + hi) * kQRows + l32];
+    }
+    const float* stat = reinterpret_cast<const float*>(img + QI::STAT);
+    l2 = stat[l32];
+    dl = stat[kQRows + l32];
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = gf[ks] = v8{};
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    asm volatile("" : "+v"(qf[ks]));
+    asm volatile("" : "+v"(gf[ks]));
+  }
+  const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
+  const float c = p.scale_log2;
+
+  // key tiles visible to some row of the workgroup
+  const int q_last = min(qr0 + qb_rows, g.lq) - 1;
+  int kv_hi = g.lk;
+  if (a.causal) kv_hi = min(kv_hi, diag + q_last + 1);
+  int kv_lo = 0;
+  if (use_window) kv_lo = max(0, diag + qr0 - a.window_left);
+  const int j_lo = kv_lo / kBKV;
+  const int j_hi = kv_hi > 0 ? (kv_hi + kBKV - 1) / kBKV : 0;
+  const int n = max(0, j_hi - j_lo);
+
+  f32x16 dq[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dq[md] = f32x16{};
+
+  v8 stg[LOADS];
+  auto tile_load = [&](int it) {
+    const v8* src = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, j_lo + it, hk, p.ntk, a.heads_kv) * KI::BYTES);
+#pragma unroll
+    for (int x = 0; x < LOADS; ++x) stg[x] = src[tid + x * kWaves * 64];
+  };
+  auto tile_store = [&](int it) {
+    v8* dst = reinterpret_cast<v8*>(smem + (it % 2) * KI::BYTES);
+#pragma unroll
+    for (int x = 0; x < LOADS; ++x) dst[tid + x * kWaves * 64] = stg[x];
+  };
+
+  auto compute = [&](int it) {
+    const int kvb = (j_lo + it) * kBKV;
+    const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * KI::BYTES);
+    // S^T[keys][rows] and dP^T
+    f32x16 s[MT], dp[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) s[mt] = dp[mt] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + l32], qf[ks], s[mt]);
+        dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + l32], gf[ks], dp[mt]);
+      }
+    // masks as ranges of the register's key offset off = key - (kvb + 4 hi)
+    const int rel = kvb + 4 * hi;
+    int hi_lim = g.lk - 1 - rel;
+    if (a.causal) hi_lim = min(hi_lim, iabs - rel);
+    const int lo_lim = use_window ? iabs - a.window_left - rel : 0;
+    const bool row_ok = i < g.lq;
+    const bool need_mask = !row_ok || hi_lim < kBKV - 1 || lo_lim > 0;
+    const float base = ALIBI ? slope2 * (float)(rel - iabs) : 0.f;
+    v8 dsf[KS2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int off = 32 * mt + 8 * (r >> 2) + (r & 3);
+        float t = s[mt][r] * c;
+        if (ALIBI) t += base + slope2 * (float)off;
+        float pv = fast_exp2(t - l2);
+        if (need_mask) pv = (row_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+        ds[r] = pv * (dp[mt][r] - dl);
+      }
+      dsf[2 * mt] = pack8<v8, T>(ds);
+      dsf[2 * mt + 1] = pack8<v8, T>(ds + 8);
+    }
+    // dQ^T += K^T dS^T
+#pragma unroll
+    for (int ks2 = 0; ks2 < KS2; ++ks2)
+#pragma unroll
+      for (int md = 0; md < MD; ++md)
+        dq[md] = mfma32(st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32], dsf[ks2], dq[md]);
+  };
+
+  if (n > 0) {
+    tile_load(0);
+    tile_store(0);
+  }
+  ring_barrier();
+  for (int it = 0; it < n; ++it) {
+    if (it + 1 < n) tile_load(it + 1);
+    compute(it);
+    if (it + 1 < n) tile_store(it + 1);
+    ring_barrier();
+  }
+
+  // ---- epilogue: lane l32 owns query row i; register (md, r) is head-dim
+  // 32 md + 8 (r/4) + 4 hi + r%4.
+  if (i >= g.lq) return;
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dq[md] *= a.softmax_scale;
+  if (a.rope_q) {
+    const int pos = min(max(a.rope_q_offset + iabs, 0), a.rope_len - 1);
+#pragma unroll
+    for (int md = 0; md < MD / 2; ++md)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
+        const float x1 = dq[md][r], x2 = dq[md + MD / 2][r];
+        dq[md][r] = x1 * cs + x2 * sn;
+        dq[md + MD / 2][r] = x2 * cs - x1 * sn;
+      }
+  }
+  T* dqrow = reinterpret_cast<T*>(p.g.dq) + (varlen ? 0 : (int64_t)b * p.g.dq_stride_b) +
+             (g.q_row0 + i) * p.g.dq_stride_t + (int64_t)hq * p.g.dq_stride_h;
+#pragma unroll
+  for (int md = 0; md < MD; ++md)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = 32 * md + 8 * gq + 4 * hi;
+      const v4 q4 = {(T)dq[md][4 * gq], (T)dq[md][4 * gq + 1], (T)dq[md][4 * gq + 2], (T)dq[md][4 * gq + 3]};
+      st_vec<v4>(dqrow + d0, q4);
+    }
+}
+
+int gcd_int(int x, int y) {
+  while (y) {
+    const int t = x % y;
+    x = y;
+    y = t;
+  }
+  return x;
+}
+
+template <typename T, int D, bool ALIBI>
+hipError_t launch_main(const BwdParams& p, hipStream_t s) {
+  const goda_prefill_args& a = p.a;
+  hipError_t e;
+  if ((e = record_timing(p.g.timing_begin, s)) != hipSuccess) return e;
+  if (a.seqlen_k > 0) {
+    auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI>;
+    const size_t lds = 2 * (size_t)QImg<D>::BYTES;
+    if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+      return e;
+    const dim3 grid((a.seqlen_k + kWaves * 32 - 1) / (kWaves * 32), a.heads_kv, a.batch);
+    kern<<<grid, kWaves * 64, lds, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (a.seqlen_q > 0) {
+    auto kern = bwd_dq_mfma_kernel<T, D, ALIBI>;
+    const size_t lds = 2 * (size_t)KVImg<D>::BYTES;
+    if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+      return e;
+    const int qb_rows = (kWaves / p.heads_per_wg) * 32;
+    const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
+    const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / p.heads_per_wg);
+    if (nblk > 0x7fffffff) return hipErrorInvalidValue;
+    kern<<<dim3((unsigned)nblk), kWaves * 64, lds, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return record_timing(p.g.timing_end, s);
+}
+
+template <typename T, int D>
+hipError_t launch_d(BwdParams p, hipStream_t s) {
+  const goda_prefill_args& a = p.a;
+  p.ntq = (a.seqlen_q + kQRows - 1) / kQRows;
+  p.ntk = (a.seqlen_k + kBKV - 1) / kBKV;
+  p.heads_per_wg = gcd_int(p.group, kWaves);
+  p.qimg = reinterpret_cast<unsigned char*>(p.g.workspace);
+  p.kvimg = p.qimg + (int64_t)a.batch * p.ntq * a.heads_q * QImg<D>::BYTES;
+  hipError_t e;
+  if (p.ntq > 0) {
+    pack_q_bwd_kernel<T, D><<<dim3(p.ntq, a.heads_q, a.batch), 256, 0, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (p.ntk > 0) {
+    pack_kv_bwd_kernel<T, D><<<dim3(p.ntk, a.heads_kv, a.batch), 256, 0, s>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (a.alibi_slopes) return launch_main<T, D, true>(p, s);
+  return launch_main<T, D, false>(p, s);
+}
+
+template <typename T>
+hipError_t launch_t(const BwdParams& p, hipStream_t s) {
+  if (p.a.head_dim == 64) return launch_d<T, 64>(p, s);
+  if (p.a.head_dim == 128) return launch_d<T, 128>(p, s);
+  return hipErrorNotSupported;
+}
+
+}  // namespace
+
+bool prefill_bwd_mfma_supported(const goda_prefill_args& a) {
+  if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16) return false;
+  return a.head_dim == 64 || a.head_dim == 128;
+}
+
+int64_t prefill_bwd_mfma_workspace_bytes(const goda_prefill_args& a) {
+  const int64_t ntq = (a.seqlen_q + kQRows - 1) / kQRows;
+  const int64_t ntk = (a.seqlen_k + kBKV - 1) / kBKV;
+  const int64_t qb = a.head_dim == 64 ? QImg<64>::BYTES : QImg<128>::BYTES;
+  const int64_t kb = a.head_dim == 64 ? KVImg<64>::BYTES : KVImg<128>::BYTES;
+  return (int64_t)a.batch * (ntq * a.heads_q * qb + ntk * a.heads_kv * kb);
+}
+
+hipError_t launch_prefill_bwd_mfma(BwdParams p, hipStream_t s) {
+  if (p.a.dtype == GODA_DTYPE_BF16) return launch_t<bf16>(p, s);
+  if (p.a.dtype == GODA_DTYPE_F16) return launch_t<f16>(p, s);
+  return hipErrorNotSupported;
+}
+
+}  // namespace goda

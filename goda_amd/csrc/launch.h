@@ -37,12 +37,20 @@ struct BwdParams {
   float scale_log2;
   int64_t delta_rows;    // row stride of the delta buffer: batch * seqlen_q
   float* delta;          // fp32 [heads_q, delta_rows]: rowsum(dO * O)
+  // MFMA path: operand images in the workspace (set by its launcher).
+  int ntq, ntk;          // 32-row query tiles / key tiles per sequence
+  int heads_per_wg;      // query heads per dq workgroup
+  unsigned char* qimg;   // [batch][ntq][heads_q] query-tile images
+  unsigned char* kvimg;  // [batch][ntk][heads_kv] key-tile images
 };
 
 // Backward: workspace bytes and the launch (generic VALU kernels for every
 // dtype; MFMA kernels for bf16/fp16 where an instance exists).
 int64_t prefill_bwd_workspace_bytes(const goda_prefill_args& a);
 hipError_t launch_prefill_bwd(const BwdParams& p, hipStream_t s);
+bool prefill_bwd_mfma_supported(const goda_prefill_args& a);
+int64_t prefill_bwd_mfma_workspace_bytes(const goda_prefill_args& a);
+hipError_t launch_prefill_bwd_mfma(BwdParams p, hipStream_t s);
 
 // Generic (VALU) prefill: any dtype, head_dim in {64,128,256}.
 hipError_t launch_prefill_generic(const PrefillParams& p, hipStream_t s);

@@ -43,29 +43,13 @@
 
 #include "common.h"
 #include "launch.h"
+#include "mfma_common.h"
 
 namespace goda {
 namespace {
 
 constexpr float kRescaleThresh = 8.0f;  // log2 units: P entries stay <= 2^8
 
-template <typename T>
-struct Vec;
-template <>
-struct Vec<bf16> {
-  typedef bf16x8 v8;
-  typedef bf16x4 v4;
-};
-template <>
-struct Vec<f16> {
-  typedef f16x8 v8;
-  typedef f16x4 v4;
-};
-
-// Position p (0..15) inside a 16-key group of the V^T image holds key
-// kPermKey(p) of that group: the P^T fragment of lane half h carries keys
-// {4h..4h+3, 8+4h..8+4h+3} of each group (accumulator rows of S^T).
-__host__ __device__ constexpr int kPermKey(int p) { return 8 * ((p % 8) / 4) + 4 * (p / 8) + p % 4; }
 
 template <int D, int BKV, int WAVES>
 struct TileGeom {
@@ -82,12 +66,6 @@ __device__ __forceinline__ int64_t ws_tile(int b, int j, int hk, int ntiles, int
   return ((int64_t)b * ntiles + j) * hkv + hk;
 }
 
-// Workgroup barrier for the tile ring. __syncthreads() would also wait for
-// every outstanding global access (vmcnt(0)), i.e. for the registers of the
-// tile being prefetched; the ring only needs this wave's LDS accesses
-// retired. The "memory" clobber keeps the compiler from moving LDS accesses
-// across it.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
 // 1. pack K (rotated) and V^T into tile images
