@@ -339,10 +339,13 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdP
     const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
     const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
 
-    // S[rows][keys]
-    f32x16 s = f32x16{};
+    // S[rows][keys] and dP[rows][keys] = dO V^T, issued together so the
+    // softmax below overlaps the dP products in flight
+    f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
     // statistics of this lane's 16 rows: 8 (r/4) + 4 hi + r%4
     f32x4 l2[4], dl[4];
 #pragma unroll
@@ -377,10 +380,6 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdP
       dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
       dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
     }
-    // dP[rows][keys] = dO V^T
-    f32x16 dp = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) ds[r] = pr[r] * (dp[r] - dl[r >> 2][r & 3]);
