@@ -60,6 +60,10 @@ struct TileGeom {
   static_assert((K_CHUNKS + V_CHUNKS) % (64 * WAVES) == 0, "tile must split evenly over the waves");
 };
 constexpr int kStages = 3;  // LDS ring: tiles j, j+1 read, tile j+2 written
+// Move each tile in two halves through half the staging registers (register
+// relief for D = 256, whose two-waves-per-SIMD form is at the limit).
+template <int D>
+constexpr bool kSplitStaging = D >= 256;
 
 // Index of workspace tile j of sequence b, KV head hk.
 __device__ __forceinline__ int64_t ws_tile(int b, int j, int hk, int ntiles, int hkv) {
@@ -400,19 +404,32 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   constexpr int LOADS = TG::LOADS_PER_LANE;
   const unsigned char* ws = reinterpret_cast<const unsigned char*>(a.workspace);
   const int my_chunk0 = wave * LOADS * 64 + lane;
-  // (Stored and later read through the same operand type v8.)
-  v8 stg[LOADS];
-  auto tile_load = [&](int j) {
+  // (Stored and later read through the same operand type v8.) With SPLIT the
+  // tile moves in two halves through half the staging registers: the first
+  // half is loaded at the start of the interval and stored mid-interval, when
+  // the second half is loaded; that one is stored at the end.
+  constexpr bool SPLIT = kSplitStaging<D> && WAVES == 8 && LOADS % 2 == 0;
+  constexpr int NSTG = SPLIT ? LOADS / 2 : LOADS;
+  v8 stg[NSTG];
+  auto tile_load_part = [&](int j, int part) {
     const v8* src = reinterpret_cast<const v8*>(ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES) +
-                    my_chunk0;
+                    my_chunk0 + part * NSTG * 64;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) stg[i] = src[i * 64];
+    for (int i = 0; i < NSTG; ++i) stg[i] = src[i * 64];
   };
-  auto tile_store = [&](int j) {
-    v8* dst = reinterpret_cast<v8*>(smem + (j % kStages) * TG::BYTES) + my_chunk0;
+  auto tile_store_part = [&](int j, int part) {
+    v8* dst = reinterpret_cast<v8*>(smem + (j % kStages) * TG::BYTES) + my_chunk0 + part * NSTG * 64;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) dst[i * 64] = stg[i];
+    for (int i = 0; i < NSTG; ++i) dst[i * 64] = stg[i];
   };
+  auto tile_load = [&](int j) {
+    tile_load_part(j, 0);
+    if constexpr (SPLIT) {
+      tile_store_part(j, 0);
+      tile_load_part(j, 1);
+    }
+  };
+  auto tile_store = [&](int j) { tile_store_part(j, SPLIT ? 1 : 0); };
 
   // This lane's K' operand for (ks, mt) is chunk (2ks + hi)*BKV + 32mt + l32;
   // its V^T operand for (ks2, md) is chunk (2ks2 + hi)*D + 32md + l32.
@@ -561,7 +578,15 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // at the end of this interval; its global loads are issued now.
   auto ring_begin = [&](int j) {
     ring_barrier();
-    if (j + 2 < j_hi) tile_load(j + 2);
+    if (j + 2 < j_hi) tile_load_part(j + 2, 0);
+  };
+  auto ring_mid = [&](int j) {
+    if constexpr (SPLIT) {
+      if (j + 2 < j_hi) {
+        tile_store_part(j + 2, 0);
+        tile_load_part(j + 2, 1);
+      }
+    }
   };
   auto ring_end = [&](int j) {
     if (j + 2 < j_hi) tile_store(j + 2);
@@ -595,9 +620,11 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       ring_begin(j);
       if (wave < 4) {
         vpart(j, s_a, pf);
+        ring_mid(j);
         mphase(j, pf, s_a);
       } else {
         mphase(j, pf, s_a);
+        ring_mid(j);
         if (j + 1 < j_hi) vpart(j + 1, s_a, pf);
       }
       ring_end(j);
