@@ -12,7 +12,7 @@
 //      product over head_dim) and transposed ([32/8][D] chunks with the rows
 //      of each 16-row group in kPermKey order, the A operand of a product
 //      over rows), plus the row statistics lse*log2(e) and delta.
-//   2. pack_kv_bwd_kernel: per (64-key tile, KV head, sequence), the
+//   2. pack_kv_bwd_kernel: per (32-key tile, KV head, sequence), the
 //      row-major images of rotated k and of v and the transposed image of k.
 //   3. bwd_dkv_mfma_kernel: one workgroup of 4 waves per 128 keys of a KV
 //      head; each wave pins the k and v operands of its 32 keys in registers
@@ -23,7 +23,8 @@
 //        dV^T [d][keys]   += dO^T P        A = dO^T image, B = P (packed S)
 //        dP   [rows][keys] = dO V^T        A = dO image,  B = v (registers)
 //        dK^T [d][keys]   += Q^T dS        A = Q^T image, B = dS (packed)
-//   4. bwd_dq_mfma_kernel: one workgroup of 4 waves per (query tile, head
+//   4. bwd_dq_mfma_kernel: one workgroup of 8 waves (two per SIMD, so one
+//      wave's products overlap the other's exp work) per (query tile, head
 //      slice); each wave pins the q and dO operands of its 32 rows and walks
 //      the key tiles:
 //        S^T  [keys][rows] = K Q^T         A = k image,   B = q (registers)
@@ -40,9 +41,10 @@
 namespace goda {
 namespace {
 
-constexpr int kQRows = 32;  // rows per query tile
-constexpr int kBKV = 64;    // keys per key tile
-constexpr int kWaves = 4;
+constexpr int kQRows = 32;   // rows per query tile
+constexpr int kBKV = 32;     // keys per key tile
+constexpr int kWaves = 4;    // dk/dv workgroup: one wave per SIMD (k, v and two accumulator sets per wave)
+constexpr int kWavesDq = 8;  // dq workgroup: two waves per SIMD
 
 template <int D>
 struct QImg {
@@ -279,7 +281,7 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdP
   v8 kf[KS], vf[KS];
   if (kw0 < g.lk) {
     const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
-    const int kin = kw0 % kBKV + l32;
+    const int kin = l32;  // the wave's 32 keys are one key tile
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + kin];
@@ -443,7 +445,7 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdP
 // 4. dq
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool ALIBI>
-__global__ void __launch_bounds__(kWaves * 64, 1) bwd_dq_mfma_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(kWavesDq * 64, 2) bwd_dq_mfma_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
   typedef QImg<D> QI;
@@ -452,14 +454,13 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dq_mfma_kernel(const BwdPa
   constexpr int MD = D / 32;
   constexpr int MT = kBKV / 32;   // 32-key blocks of S^T
   constexpr int KS2 = kBKV / 16;  // k-steps of dQ^T over keys
-  constexpr int LOADS = KI::CHUNKS / (kWaves * 64);
-  static_assert(KI::CHUNKS % (kWaves * 64) == 0, "tile must split over the waves");
+  constexpr int LOADS = (KI::CHUNKS + kWavesDq * 64 - 1) / (kWavesDq * 64);
   extern __shared__ __align__(16) unsigned char smem[];
 
   const goda_prefill_args& a = p.a;
   const int hg = p.heads_per_wg;
   const int nslices = p.group / hg;
-  const int qb_rows = (kWaves / hg) * 32;
+  const int qb_rows = (kWavesDq / hg) * 32;
   const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
   const int lin = blockIdx.x;
   const int pair = lin / nqt;
@@ -525,12 +526,14 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dq_mfma_kernel(const BwdPa
   auto tile_load = [&](int it) {
     const v8* src = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, j_lo + it, hk, p.ntk, a.heads_kv) * KI::BYTES);
 #pragma unroll
-    for (int x = 0; x < LOADS; ++x) stg[x] = src[tid + x * kWaves * 64];
+    for (int x = 0; x < LOADS; ++x)
+      if (KI::CHUNKS % (kWavesDq * 64) == 0 || tid + x * kWavesDq * 64 < KI::CHUNKS) stg[x] = src[tid + x * kWavesDq * 64];
   };
   auto tile_store = [&](int it) {
     v8* dst = reinterpret_cast<v8*>(smem + (it % 2) * KI::BYTES);
 #pragma unroll
-    for (int x = 0; x < LOADS; ++x) dst[tid + x * kWaves * 64] = stg[x];
+    for (int x = 0; x < LOADS; ++x)
+      if (KI::CHUNKS % (kWavesDq * 64) == 0 || tid + x * kWavesDq * 64 < KI::CHUNKS) dst[tid + x * kWavesDq * 64] = stg[x];
   };
 
   auto compute = [&](int it) {
@@ -649,11 +652,11 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
     const size_t lds = 2 * (size_t)KVImg<D>::BYTES;
     if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
       return e;
-    const int qb_rows = (kWaves / p.heads_per_wg) * 32;
+    const int qb_rows = (kWavesDq / p.heads_per_wg) * 32;
     const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
     const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / p.heads_per_wg);
     if (nblk > 0x7fffffff) return hipErrorInvalidValue;
-    kern<<<dim3((unsigned)nblk), kWaves * 64, lds, s>>>(p);
+    kern<<<dim3((unsigned)nblk), kWavesDq * 64, lds, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return record_timing(p.g.timing_end, s);
@@ -664,7 +667,7 @@ hipError_t launch_d(BwdParams p, hipStream_t s) {
   const goda_prefill_args& a = p.a;
   p.ntq = (a.seqlen_q + kQRows - 1) / kQRows;
   p.ntk = (a.seqlen_k + kBKV - 1) / kBKV;
-  p.heads_per_wg = gcd_int(p.group, kWaves);
+  p.heads_per_wg = gcd_int(p.group, kWavesDq);
   p.qimg = reinterpret_cast<unsigned char*>(p.g.workspace);
   p.kvimg = p.qimg + (int64_t)a.batch * p.ntq * a.heads_q * QImg<D>::BYTES;
   hipError_t e;
