@@ -14,11 +14,12 @@
 //      over rows), plus the row statistics lse*log2(e) and delta.
 //   2. pack_kv_bwd_kernel: per (32-key tile, KV head, sequence), the
 //      row-major images of rotated k and of v and the transposed image of k.
-//   3. bwd_dkv_mfma_kernel: one workgroup of 4 waves per 128 keys of a KV
-//      head; each wave pins the k and v operands of its 32 keys in registers
-//      and walks the query tiles of every head of the group (GQA reduction in
-//      the accumulators, no atomics), the tiles moving through a two-stage
-//      LDS ring:
+//   3. bwd_dkv_mfma_kernel: one workgroup of 8 waves per 128 keys of a KV
+//      head, in pairs (two waves of one SIMD) that share 32 keys; the pair
+//      pins the k and v operands of its keys and walks the query tiles of
+//      every head of the group (GQA reduction in the accumulators, no
+//      atomics), the tiles moving through a three-stage LDS ring. One wave
+//      of a pair computes S, P and dV, the other dP, dS and dK:
 //        S    [rows][keys] = Q K^T        A = Q image,   B = k (registers)
 //        dV^T [d][keys]   += dO^T P        A = dO^T image, B = P (packed S)
 //        dP   [rows][keys] = dO V^T        A = dO image,  B = v (registers)
@@ -43,7 +44,6 @@ namespace {
 
 constexpr int kQRows = 32;   // rows per query tile
 constexpr int kBKV = 32;     // keys per key tile
-constexpr int kWaves = 4;    // dk/dv workgroup: one wave per SIMD (k, v and two accumulator sets per wave)
 constexpr int kWavesDq = 8;  // dq workgroup: two waves per SIMD
 
 template <int D>
@@ -250,59 +250,72 @@ __device__ __forceinline__ V pack8(const float* x) {
 // ---------------------------------------------------------------------------
 // 3. dk, dv
 // ---------------------------------------------------------------------------
+// Eight waves, two per SIMD, in pairs that share 32 keys: wave w < 4 ("A")
+// pins k and computes S, P and dV^T += dO^T P; wave w + 4 ("B", same SIMD)
+// pins v and computes dP and, one query tile later, dS = P (dP - delta) with
+// A's P read back from LDS, and dK^T += Q^T dS. Query tiles move through a
+// three-stage ring so that B's previous tile is still resident.
+constexpr int kWavesKv = 8;
+constexpr int kKvStages = 3;
+
+template <int D>
+struct DkvSmem {
+  static constexpr int64_t RING = kKvStages * QImg<D>::BYTES;
+  // P exchange: [parity][pair][register group][lane] f32x4
+  static constexpr int64_t PBUF = 2 * 4 * 4 * 64 * 16;
+  static constexpr int64_t BYTES = RING + PBUF;
+};
+
 template <typename T, int D, bool ALIBI>
-__global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
   typedef QImg<D> QI;
   typedef KVImg<D> KI;
   constexpr int KS = D / 16;  // k-steps over head_dim
   constexpr int MD = D / 32;  // 32-wide head_dim tiles of dK^T / dV^T
-  constexpr int LOADS = 4 * QI::CH / (kWaves * 64);
-  static_assert(4 * QI::CH % (kWaves * 64) == 0, "tile must split over the waves");
+  constexpr int LOADS = 4 * QI::CH / (kWavesKv * 64);
+  static_assert(4 * QI::CH % (kWavesKv * 64) == 0, "tile must split over the waves");
   extern __shared__ __align__(16) unsigned char smem[];
+  f32x4* pbuf = reinterpret_cast<f32x4*>(smem + DkvSmem<D>::RING);
 
   const goda_prefill_args& a = p.a;
   const int b = blockIdx.z, hk = blockIdx.y;
   const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
   const bool varlen = a.cu_seqlens_k != nullptr;
   const int kend = varlen ? g.lk : a.seqlen_k;  // rows this launch writes
-  const int kv0 = blockIdx.x * (kWaves * 32);
+  const int kv0 = blockIdx.x * 128;
   if (kv0 >= kend) return;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
-  const int kw0 = kv0 + 32 * wave;
+  const bool role_b = wave >= 4;  // wave-uniform
+  const int pair = wave & 3;
+  const int kw0 = kv0 + 32 * pair;
   const int key = kw0 + l32;
   const int diag = g.lk - g.lq;
   const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
 
-  // B operands of this wave's 32 keys: k (rotated) and v rows, from the images.
-  v8 kf[KS], vf[KS];
+  // B operand of this wave's 32 keys: k (A) or v (B), from the key images.
+  v8 bf[KS];
   if (kw0 < g.lk) {
     const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
-    const int kin = l32;  // the wave's 32 keys are one key tile
+    const int base = role_b ? KI::VA : KI::KA;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + kin];
-      vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + kin];
-    }
+    for (int ks = 0; ks < KS; ++ks) bf[ks] = img[base + (2 * ks + hi) * kBKV + l32];
   } else {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = vf[ks] = v8{};
+    for (int ks = 0; ks < KS; ++ks) bf[ks] = v8{};
   }
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    asm volatile("" : "+v"(kf[ks]));
-    asm volatile("" : "+v"(vf[ks]));
-  }
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(bf[ks]));
 
-  f32x16 dk[MD], dv[MD];
+  f32x16 acc[MD];  // dV^T (A) or dK^T (B)
 #pragma unroll
-  for (int md = 0; md < MD; ++md) dk[md] = dv[md] = f32x16{};
+  for (int md = 0; md < MD; ++md) acc[md] = f32x16{};
 
   // Query tiles that can see a key of this workgroup.
-  const int kv_last = min(kv0 + kWaves * 32, g.lk) - 1;
+  const int kv_last = min(kv0 + 128, g.lk) - 1;
   int i_lo = 0, i_hi = g.lq;
   if (a.causal) i_lo = max(0, kv0 - diag);
   if (use_window) i_hi = min(g.lq, kv_last + a.window_left - diag + 1);
@@ -311,133 +324,151 @@ __global__ void __launch_bounds__(kWaves * 64, 1) bwd_dkv_mfma_kernel(const BwdP
   const int nq = i_hi > i_lo ? (i_hi - 1) / kQRows + 1 - qt_lo : 0;
   const int n = p.group * nq;
 
-  // two-stage ring of query tiles: the main images (LOADS chunks per lane)
-  // plus the 16 statistics chunks (lanes 0..15 of wave 0)
   v8 stg[LOADS];
   v8 stg_stat;
-  auto tile_src = [&](int it) {
+  auto tile_load = [&](int it) {
     const int hq = hk * p.group + it / nq;
     const int qt = qt_lo + it % nq;
-    return reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
-  };
-  auto tile_load = [&](int it) {
-    const v8* src = tile_src(it);
+    const v8* src = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) stg[i] = src[tid + i * kWaves * 64];
+    for (int i = 0; i < LOADS; ++i) stg[i] = src[tid + i * kWavesKv * 64];
     if (tid < 16) stg_stat = src[QI::STAT + tid];
   };
   auto tile_store = [&](int it) {
-    v8* dst = reinterpret_cast<v8*>(smem + (it % 2) * QI::BYTES);
+    v8* dst = reinterpret_cast<v8*>(smem + (it % kKvStages) * QI::BYTES);
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) dst[tid + i * kWaves * 64] = stg[i];
+    for (int i = 0; i < LOADS; ++i) dst[tid + i * kWavesKv * 64] = stg[i];
     if (tid < 16) dst[QI::STAT + tid] = stg_stat;
   };
+  auto stage = [&](int it) { return reinterpret_cast<const v8*>(smem + (it % kKvStages) * QI::BYTES); };
 
   const float c = p.scale_log2;
-  auto compute = [&](int it) {
+  // A: S, P (to LDS), dV^T += dO^T P for tile it.
+  auto part_a = [&](int it) {
     const int hq = hk * p.group + it / nq;
     const int q0 = (qt_lo + it % nq) * kQRows;
     const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
-    const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
+    const v8* st = stage(it);
     const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
-
-    // S[rows][keys] and dP[rows][keys] = dO V^T, issued together so the
-    // softmax below overlaps the dP products in flight
-    f32x16 s = f32x16{}, dp = f32x16{};
+    f32x16 s = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
-    // statistics of this lane's 16 rows: 8 (r/4) + 4 hi + r%4
-    f32x4 l2[4], dl[4];
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      l2[gq] = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
-      dl[gq] = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
-    }
-    // Visibility as a range of the register's row offset off = row - (q0 + 4 hi):
-    // causal key <= diag + row, window diag + row - key <= W, row < lq, key < lk.
+    for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], bf[ks], s);
+    // Visibility as a range of the register's row offset off = row - (q0 + 4 hi).
     const int rel = q0 + 4 * hi;
     int lo_lim = -1, hi_lim = g.lq - 1 - rel;
     if (a.causal) lo_lim = key - diag - rel;
     if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
     const bool key_ok = key < g.lk;
-    const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27 || kw0 + 31 >= g.lk;
-    // bias slope * (key - diag - row) = base - slope * off
+    const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27;
     const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
+    f32x4 pr4[4];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * gq + e;
+        const int off = 8 * gq + e;
+        float t = s[r] * c;
+        if (ALIBI) t += base - slope2 * (float)off;
+        float pv = fast_exp2(t - l2[e]);
+        if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+        pr4[gq][e] = pv;
+      }
+      pbuf[((it & 1) * 4 + pair) * 4 * 64 + gq * 64 + lane] = pr4[gq];
+    }
     float pr[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int off = 8 * (r >> 2) + (r & 3);
-      float t = s[r] * c;
-      if (ALIBI) t += base - slope2 * (float)off;
-      float pv = fast_exp2(t - l2[r >> 2][r & 3]);
-      if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
-      pr[r] = pv;
-    }
-    // dV^T += dO^T P
-    v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
+    for (int r = 0; r < 16; ++r) pr[r] = pr4[r >> 2][r & 3];
+    const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
-      dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
-      dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
+      acc[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, acc[md]);
+      acc[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, acc[md]);
     }
+  };
+  // B: dP for tile it.
+  auto part_b_dp = [&](int it) {
+    const v8* st = stage(it);
+    f32x16 dp = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], bf[ks], dp);
+    return dp;
+  };
+  // B: dS and dK^T += Q^T dS for tile it (P of tile it from LDS).
+  auto part_b_dk = [&](int it, const f32x16& dp) {
+    const v8* st = stage(it);
+    const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
     float ds[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ds[r] = pr[r] * (dp[r] - dl[r >> 2][r & 3]);
-    v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
-    // dK^T += Q^T dS
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 pv = pbuf[((it & 1) * 4 + pair) * 4 * 64 + gq * 64 + lane];
+      const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ds[4 * gq + e] = pv[e] * (dp[4 * gq + e] - dl[e]);
+    }
+    const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
-      dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
-      dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
+      acc[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, acc[md]);
+      acc[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, acc[md]);
     }
   };
 
+  // Iteration it: A handles tile it; B computes dP of tile it and finishes
+  // tile it - 1. Stages in use: (it - 1) % 3 and it % 3; tile it + 1 is
+  // loaded at the start and stored at the end into the third stage.
   if (n > 0) {
     tile_load(0);
     tile_store(0);
   }
-  ring_barrier();
-  for (int it = 0; it < n; ++it) {
-    if (it + 1 < n) tile_load(it + 1);
-    compute(it);
-    if (it + 1 < n) tile_store(it + 1);
+  f32x16 dp_prev = f32x16{};
+  for (int it = 0; it <= n; ++it) {
     ring_barrier();
+    if (it + 1 < n) tile_load(it + 1);
+    if (!role_b) {
+      if (it < n) part_a(it);
+    } else {
+      f32x16 dp_cur = f32x16{};
+      if (it < n) dp_cur = part_b_dp(it);
+      if (it > 0) part_b_dk(it - 1, dp_prev);
+      dp_prev = dp_cur;
+    }
+    if (it + 1 < n) tile_store(it + 1);
   }
 
   // ---- epilogue: lane l32 owns key row `key`; register (md, r) is head-dim
-  // 32 md + 8 (r/4) + 4 hi + r%4.
+  // 32 md + 8 (r/4) + 4 hi + r%4. A writes dV, B writes dK.
   if (key >= kend) return;
+  if (role_b) {
 #pragma unroll
-  for (int md = 0; md < MD; ++md) dk[md] *= a.softmax_scale;
-  if (a.rope_k && key < g.lk) {
-    // transpose of the rotation: pairs (d, d + D/2) are blocks md, md + MD/2
-    const int pos = a.rope_k_offset + key;
+    for (int md = 0; md < MD; ++md) acc[md] *= a.softmax_scale;
+    if (a.rope_k && key < g.lk) {
+      // transpose of the rotation: pairs (d, d + D/2) are blocks md, md + MD/2
+      const int pos = a.rope_k_offset + key;
 #pragma unroll
-    for (int md = 0; md < MD / 2; ++md)
+      for (int md = 0; md < MD / 2; ++md)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
-        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
-        const float x1 = dk[md][r], x2 = dk[md + MD / 2][r];
-        dk[md][r] = x1 * cs + x2 * sn;
-        dk[md + MD / 2][r] = x2 * cs - x1 * sn;
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
+          const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
+          const float x1 = acc[md][r], x2 = acc[md + MD / 2][r];
+          acc[md][r] = x1 * cs + x2 * sn;
+          acc[md + MD / 2][r] = x2 * cs - x1 * sn;
+        }
+    }
   }
-  T* dkrow = reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
-             (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h;
-  T* dvrow = reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
-             (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
+  T* row = role_b ? reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
+                        (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h
+                  : reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
+                        (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
 #pragma unroll
   for (int md = 0; md < MD; ++md)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const int d0 = 32 * md + 8 * gq + 4 * hi;
-      const v4 kv4 = {(T)dk[md][4 * gq], (T)dk[md][4 * gq + 1], (T)dk[md][4 * gq + 2], (T)dk[md][4 * gq + 3]};
-      const v4 vv4 = {(T)dv[md][4 * gq], (T)dv[md][4 * gq + 1], (T)dv[md][4 * gq + 2], (T)dv[md][4 * gq + 3]};
-      st_vec<v4>(dkrow + d0, kv4);
-      st_vec<v4>(dvrow + d0, vv4);
+      const v4 x4 = {(T)acc[md][4 * gq], (T)acc[md][4 * gq + 1], (T)acc[md][4 * gq + 2], (T)acc[md][4 * gq + 3]};
+      st_vec<v4>(row + d0, x4);
     }
 }
 
@@ -640,11 +671,11 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
   if ((e = record_timing(p.g.timing_begin, s)) != hipSuccess) return e;
   if (a.seqlen_k > 0) {
     auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI>;
-    const size_t lds = 2 * (size_t)QImg<D>::BYTES;
+    const size_t lds = (size_t)DkvSmem<D>::BYTES;
     if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
       return e;
-    const dim3 grid((a.seqlen_k + kWaves * 32 - 1) / (kWaves * 32), a.heads_kv, a.batch);
-    kern<<<grid, kWaves * 64, lds, s>>>(p);
+    const dim3 grid((a.seqlen_k + 127) / 128, a.heads_kv, a.batch);
+    kern<<<grid, kWavesKv * 64, lds, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (a.seqlen_q > 0) {
