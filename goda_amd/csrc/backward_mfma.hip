@@ -1,5 +1,5 @@
 // Backward of prefill attention on gfx950 matrix cores: bf16 / fp16 operands,
-// fp32 accumulation, head_dim 64 or 128 (others take the generic kernels).
+// fp32 accumulation, head_dim 64, 128 or 256 (others take the generic kernels).
 // Same quantities as kernels_/flash_attn_gqa/cuda.py:6-246:
 //   P = exp(scale q k^T + bias - lse), dV = P^T dO, dP = dO V^T,
 //   dS = P * (dP - delta) with delta = rowsum(dO * O),
@@ -24,16 +24,23 @@
 //        dV^T [d][keys]   += dO^T P        A = dO^T image, B = P (packed S)
 //        dP   [rows][keys] = dO V^T        A = dO image,  B = v (registers)
 //        dK^T [d][keys]   += Q^T dS        A = Q^T image, B = dS (packed)
+//      head_dim 256 (bwd_dkv_wide_kernel): a wave needs both operand sets and
+//      both accumulators (~450 registers), so four waves, one per SIMD, each
+//      owning 32 keys and doing all four products; with few key blocks the
+//      walk is split over several workgroups whose fp32 partials
+//      bwd_dkv_reduce_kernel sums.
 //   4. bwd_dq_mfma_kernel: one workgroup of 8 waves (two per SIMD, so one
-//      wave's products overlap the other's exp work) per (query tile, head
-//      slice); each wave pins the q and dO operands of its 32 rows and walks
-//      the key tiles:
+//      wave's products overlap the other's exp work; 4 waves, one per SIMD,
+//      at head_dim 256) per (query tile, head slice); each wave pins the q and
+//      dO operands of its 32 rows and walks the key tiles:
 //        S^T  [keys][rows] = K Q^T         A = k image,   B = q (registers)
 //        dP^T [keys][rows] = V dO^T        A = v image,   B = dO (registers)
 //        dQ^T [d][rows]   += K^T dS^T      A = K^T image, B = dS^T (packed)
 // A packed accumulator becomes a B operand directly because the transposed
 // images hold their rows / keys in the accumulator's register order
 // (kPermKey). With the log-sum-exp known there is no online softmax.
+
+#include <algorithm>
 
 #include "common.h"
 #include "launch.h"
@@ -44,7 +51,13 @@ namespace {
 
 constexpr int kQRows = 32;   // rows per query tile
 constexpr int kBKV = 32;     // keys per key tile
-constexpr int kWavesDq = 8;  // dq workgroup: two waves per SIMD
+// dq workgroup: two waves per SIMD, or one at head_dim 256 (q and dO operands
+// plus the dQ^T accumulator take ~350 registers there).
+template <int D>
+struct DqShape {
+  static constexpr int WAVES = D >= 256 ? 4 : 8;
+  static constexpr int OCC = D >= 256 ? 1 : 2;
+};
 
 template <int D>
 struct QImg {
@@ -473,10 +486,297 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
 }
 
 // ---------------------------------------------------------------------------
+// 3b. dk, dv at head_dim 256
+// ---------------------------------------------------------------------------
+// Four waves, one per SIMD: each owns 32 keys, pins their k and v operands
+// (2 x 64 registers) and accumulates dK^T and dV^T (2 x 128 registers), and
+// per query tile computes S, dP, P, dS and both products itself. Query tiles
+// (64 KB of images each) move through a two-stage LDS ring, staged through
+// registers in four parts issued between the four product phases. Workgroup
+// (key block, hk * nsplit + split) walks its share of the (query head, query
+// tile) pairs; with nsplit > 1 it writes fp32 partials.
+constexpr int kWavesWide = 4;
+constexpr int kWideParts = 4;
+
+// Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
+// run LEAD MFMAs ahead (not all hoisted, which would hold 4 registers each).
+template <int NM, int LEAD>
+__device__ __forceinline__ void lead_schedule() {
+  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);
+#pragma unroll
+  for (int i = 0; i < NM - LEAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+}
+
+template <typename T, int D, bool ALIBI>
+__global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const BwdParams p) {
+  typedef typename Vec<T>::v8 v8;
+  typedef typename Vec<T>::v4 v4;
+  typedef QImg<D> QI;
+  typedef KVImg<D> KI;
+  constexpr int KS = D / 16;
+  constexpr int MD = D / 32;
+  constexpr int NTH = kWavesWide * 64;
+  constexpr int LOADS = 4 * QI::CH / NTH;
+  constexpr int PART = LOADS / kWideParts;
+  static_assert(4 * QI::CH % (NTH * kWideParts) == 0, "tile must split over the threads and parts");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const goda_prefill_args& a = p.a;
+  const int b = blockIdx.z;
+  const int hk = blockIdx.y / p.nsplit, split = blockIdx.y % p.nsplit;
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  const bool varlen = a.cu_seqlens_k != nullptr;
+  const int kend = varlen ? g.lk : a.seqlen_k;  // rows this launch writes
+  const int kv0 = blockIdx.x * 32 * kWavesWide;
+  if (kv0 >= kend) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int kw0 = kv0 + 32 * wave;
+  const int key = kw0 + l32;
+  const int diag = g.lk - g.lq;
+  const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
+
+  v8 kf[KS], vf[KS];
+  if (kw0 < g.lk) {
+    const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + l32];
+      vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + l32];
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = vf[ks] = v8{};
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    asm volatile("" : "+v"(kf[ks]));
+    asm volatile("" : "+v"(vf[ks]));
+  }
+  f32x16 dv[MD], dk[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dv[md] = dk[md] = f32x16{};
+
+  // Query tiles that can see a key of this workgroup, and this split's share.
+  const int kv_last = min(kv0 + 32 * kWavesWide, g.lk) - 1;
+  int i_lo = 0, i_hi = g.lq;
+  if (a.causal) i_lo = max(0, kv0 - diag);
+  if (use_window) i_hi = min(g.lq, kv_last + a.window_left - diag + 1);
+  if (kv0 >= g.lk) i_hi = i_lo;
+  const int qt_lo = i_lo / kQRows;
+  const int nq = i_hi > i_lo ? (i_hi - 1) / kQRows + 1 - qt_lo : 0;
+  const int n = p.group * nq;
+  const int it0 = (int)((int64_t)n * split / p.nsplit);
+  const int it1 = (int)((int64_t)n * (split + 1) / p.nsplit);
+
+  v8 stg[PART];
+  v8 stg_stat;
+  auto src_of = [&](int it) {
+    const int hq = hk * p.group + it / nq;
+    const int qt = qt_lo + it % nq;
+    return reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
+  };
+  auto load_part = [&](int it, int part) {
+    const v8* src = src_of(it);
+#pragma unroll
+    for (int i = 0; i < PART; ++i) stg[i] = src[tid + (part * PART + i) * NTH];
+    if (part == 0 && tid < 16) stg_stat = src[QI::STAT + tid];
+  };
+  auto store_part = [&](int it, int part) {
+    v8* dst = reinterpret_cast<v8*>(smem + (it % 2) * QI::BYTES);
+#pragma unroll
+    for (int i = 0; i < PART; ++i) dst[tid + (part * PART + i) * NTH] = stg[i];
+    if (part == 0 && tid < 16) dst[QI::STAT + tid] = stg_stat;
+  };
+
+  const float c = p.scale_log2;
+  if (it0 < it1) {
+#pragma unroll
+    for (int part = 0; part < kWideParts; ++part) {
+      load_part(it0, part);
+      store_part(it0, part);
+    }
+  }
+  ring_barrier();
+  for (int it = it0; it < it1; ++it) {
+    const bool more = it + 1 < it1;
+    const int hq = hk * p.group + it / nq;
+    const int q0 = (qt_lo + it % nq) * kQRows;
+    const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
+    const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
+    const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
+
+    if (more) load_part(it + 1, 0);
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
+    lead_schedule<KS, 4>();
+    if (more) {
+      store_part(it + 1, 0);
+      load_part(it + 1, 1);
+    }
+    f32x16 dp = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
+    lead_schedule<KS, 4>();
+
+    // P and dS; visibility as a range of the register's row offset
+    // off = row - (q0 + 4 hi).
+    const int rel = q0 + 4 * hi;
+    int lo_lim = -1, hi_lim = g.lq - 1 - rel;
+    if (a.causal) lo_lim = key - diag - rel;
+    if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
+    const bool key_ok = key < g.lk;
+    const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27;
+    const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
+    float pr[16], ds[16];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
+      const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * gq + e;
+        const int off = 8 * gq + e;
+        float t = s[r] * c;
+        if (ALIBI) t += base - slope2 * (float)off;
+        float pv = fast_exp2(t - l2[e]);
+        if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+        pr[r] = pv;
+        ds[r] = pv * (dp[r] - dl[e]);
+      }
+    }
+    if (more) {
+      store_part(it + 1, 1);
+      load_part(it + 1, 2);
+    }
+    const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
+#pragma unroll
+    for (int md = 0; md < MD; ++md) {
+      dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
+      dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
+    }
+    lead_schedule<2 * MD, 4>();
+    if (more) {
+      store_part(it + 1, 2);
+      load_part(it + 1, 3);
+    }
+    const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
+#pragma unroll
+    for (int md = 0; md < MD; ++md) {
+      dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
+      dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
+    }
+    lead_schedule<2 * MD, 4>();
+    if (more) store_part(it + 1, 3);
+    ring_barrier();
+  }
+
+  // ---- epilogue: lane l32 owns key row `key`; register (md, r) is head-dim
+  // 32 md + 8 (r/4) + 4 hi + r%4.
+  if (key >= kend) return;
+  if (p.nsplit > 1) {
+    const int64_t rows = (int64_t)a.batch * a.seqlen_k;
+    const int64_t row = (int64_t)b * a.seqlen_k + key;
+    float* pk = p.part + (((int64_t)(2 * split) * rows + row) * a.heads_kv + hk) * D;
+    float* pv = p.part + (((int64_t)(2 * split + 1) * rows + row) * a.heads_kv + hk) * D;
+#pragma unroll
+    for (int md = 0; md < MD; ++md)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d0 = 32 * md + 8 * gq + 4 * hi;
+        st_vec<f32x4>(pk + d0, f32x4{dk[md][4 * gq], dk[md][4 * gq + 1], dk[md][4 * gq + 2], dk[md][4 * gq + 3]});
+        st_vec<f32x4>(pv + d0, f32x4{dv[md][4 * gq], dv[md][4 * gq + 1], dv[md][4 * gq + 2], dv[md][4 * gq + 3]});
+      }
+    return;
+  }
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dk[md] *= a.softmax_scale;
+  if (a.rope_k && key < g.lk) {
+    const int pos = a.rope_k_offset + key;
+#pragma unroll
+    for (int md = 0; md < MD / 2; ++md)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
+        const float x1 = dk[md][r], x2 = dk[md + MD / 2][r];
+        dk[md][r] = x1 * cs + x2 * sn;
+        dk[md + MD / 2][r] = x2 * cs - x1 * sn;
+      }
+  }
+  T* krow = reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
+            (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h;
+  T* vrow = reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
+            (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
+#pragma unroll
+  for (int md = 0; md < MD; ++md)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = 32 * md + 8 * gq + 4 * hi;
+      st_vec<v4>(krow + d0, v4{(T)dk[md][4 * gq], (T)dk[md][4 * gq + 1], (T)dk[md][4 * gq + 2], (T)dk[md][4 * gq + 3]});
+      st_vec<v4>(vrow + d0, v4{(T)dv[md][4 * gq], (T)dv[md][4 * gq + 1], (T)dv[md][4 * gq + 2], (T)dv[md][4 * gq + 3]});
+    }
+}
+
+// Sum of the nsplit fp32 partials of dk and dv; dk scaled and rotated back.
+// One thread per (key, 4 head-dims of the first half and their RoPE partners).
+template <typename T, int D>
+__global__ void __launch_bounds__(256) bwd_dkv_reduce_kernel(const BwdParams p) {
+  typedef typename Vec<T>::v4 v4;
+  const goda_prefill_args& a = p.a;
+  const int b = blockIdx.z, hk = blockIdx.y;
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  const bool varlen = a.cu_seqlens_k != nullptr;
+  const int kend = varlen ? g.lk : a.seqlen_k;
+  constexpr int G = D / 8;  // groups of 4 head-dims in the first half
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int key = (int)(idx / G);
+  const int d0 = (int)(idx % G) * 4;
+  if (key >= kend) return;
+  const int64_t rows = (int64_t)a.batch * a.seqlen_k;
+  const int64_t row = (int64_t)b * a.seqlen_k + key;
+  f32x4 k1 = {}, k2 = {}, v1 = {}, v2 = {};
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float* pk = p.part + (((int64_t)(2 * s) * rows + row) * a.heads_kv + hk) * D;
+    const float* pv = p.part + (((int64_t)(2 * s + 1) * rows + row) * a.heads_kv + hk) * D;
+    k1 += ld_vec<f32x4>(pk + d0);
+    k2 += ld_vec<f32x4>(pk + d0 + D / 2);
+    v1 += ld_vec<f32x4>(pv + d0);
+    v2 += ld_vec<f32x4>(pv + d0 + D / 2);
+  }
+  k1 *= a.softmax_scale;
+  k2 *= a.softmax_scale;
+  if (a.rope_k && key < g.lk) {
+    const int pos = a.rope_k_offset + key;
+    const f32x4 cs = ld_vec<f32x4>(a.rope_cos + (int64_t)pos * (D / 2) + d0);
+    const f32x4 sn = ld_vec<f32x4>(a.rope_sin + (int64_t)pos * (D / 2) + d0);
+    const f32x4 y1 = k1 * cs + k2 * sn;
+    const f32x4 y2 = k2 * cs - k1 * sn;
+    k1 = y1;
+    k2 = y2;
+  }
+  T* krow = reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
+            (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h;
+  T* vrow = reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
+            (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
+  st_vec<v4>(krow + d0, v4{(T)k1[0], (T)k1[1], (T)k1[2], (T)k1[3]});
+  st_vec<v4>(krow + d0 + D / 2, v4{(T)k2[0], (T)k2[1], (T)k2[2], (T)k2[3]});
+  st_vec<v4>(vrow + d0, v4{(T)v1[0], (T)v1[1], (T)v1[2], (T)v1[3]});
+  st_vec<v4>(vrow + d0 + D / 2, v4{(T)v2[0], (T)v2[1], (T)v2[2], (T)v2[3]});
+}
+
+// ---------------------------------------------------------------------------
 // 4. dq
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool ALIBI>
-__global__ void __launch_bounds__(kWavesDq * 64, 2) bwd_dq_mfma_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(DqShape<D>::WAVES * 64, DqShape<D>::OCC) bwd_dq_mfma_kernel(const BwdParams p) {
+  constexpr int kWavesDq = DqShape<D>::WAVES;
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
   typedef QImg<D> QI;
@@ -670,19 +970,35 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
   hipError_t e;
   if ((e = record_timing(p.g.timing_begin, s)) != hipSuccess) return e;
   if (a.seqlen_k > 0) {
-    auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI>;
-    const size_t lds = (size_t)DkvSmem<D>::BYTES;
-    if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
-      return e;
-    const dim3 grid((a.seqlen_k + 127) / 128, a.heads_kv, a.batch);
-    kern<<<grid, kWavesKv * 64, lds, s>>>(p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if constexpr (D >= 256) {
+      auto kern = bwd_dkv_wide_kernel<T, D, ALIBI>;
+      const size_t lds = 2 * (size_t)QImg<D>::BYTES;
+      if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+        return e;
+      const dim3 grid((a.seqlen_k + 32 * kWavesWide - 1) / (32 * kWavesWide), a.heads_kv * p.nsplit, a.batch);
+      kern<<<grid, kWavesWide * 64, lds, s>>>(p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      if (p.nsplit > 1) {
+        const int64_t threads = (int64_t)a.seqlen_k * (D / 8);
+        bwd_dkv_reduce_kernel<T, D><<<dim3((unsigned)((threads + 255) / 256), a.heads_kv, a.batch), 256, 0, s>>>(p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+      }
+    } else {
+      auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI>;
+      const size_t lds = (size_t)DkvSmem<D>::BYTES;
+      if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
+        return e;
+      const dim3 grid((a.seqlen_k + 127) / 128, a.heads_kv, a.batch);
+      kern<<<grid, kWavesKv * 64, lds, s>>>(p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
   }
   if (a.seqlen_q > 0) {
     auto kern = bwd_dq_mfma_kernel<T, D, ALIBI>;
     const size_t lds = 2 * (size_t)KVImg<D>::BYTES;
     if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
       return e;
+    constexpr int kWavesDq = DqShape<D>::WAVES;
     const int qb_rows = (kWavesDq / p.heads_per_wg) * 32;
     const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
     const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / p.heads_per_wg);
@@ -693,14 +1009,40 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
   return record_timing(p.g.timing_end, s);
 }
 
+// Workgroups per key block of the head_dim-256 dk/dv kernel: enough that the
+// grid holds ~1024 workgroups (MQA and short batches have few key blocks, and
+// causal key blocks differ in work by up to the sequence length), at most 8
+// and at most the (query head, query tile) pairs a key block can see.
+int dkv_splits(const goda_prefill_args& a) {
+  if (a.head_dim < 256 || a.heads_kv <= 0) return 1;
+  const int64_t wgs = (int64_t)((a.seqlen_k + 32 * kWavesWide - 1) / (32 * kWavesWide)) * a.heads_kv * a.batch;
+  if (wgs <= 0) return 1;
+  int64_t ns = (1024 + wgs - 1) / wgs;
+  const int64_t pairs = (int64_t)(a.heads_q / a.heads_kv) * ((a.seqlen_q + kQRows - 1) / kQRows);
+  ns = std::min<int64_t>(ns, std::max<int64_t>(1, pairs));
+  return (int)std::min<int64_t>(ns, 8);
+}
+
+template <int D>
+int64_t workspace_bytes_d(const goda_prefill_args& a) {
+  const int64_t ntq = (a.seqlen_q + kQRows - 1) / kQRows;
+  const int64_t ntk = (a.seqlen_k + kBKV - 1) / kBKV;
+  int64_t bytes = (int64_t)a.batch * (ntq * a.heads_q * QImg<D>::BYTES + ntk * a.heads_kv * KVImg<D>::BYTES);
+  const int ns = dkv_splits(a);
+  if (ns > 1) bytes += (int64_t)ns * 2 * a.batch * a.seqlen_k * a.heads_kv * D * 4;
+  return bytes;
+}
+
 template <typename T, int D>
 hipError_t launch_d(BwdParams p, hipStream_t s) {
   const goda_prefill_args& a = p.a;
   p.ntq = (a.seqlen_q + kQRows - 1) / kQRows;
   p.ntk = (a.seqlen_k + kBKV - 1) / kBKV;
-  p.heads_per_wg = gcd_int(p.group, kWavesDq);
+  p.heads_per_wg = gcd_int(p.group, DqShape<D>::WAVES);
   p.qimg = reinterpret_cast<unsigned char*>(p.g.workspace);
   p.kvimg = p.qimg + (int64_t)a.batch * p.ntq * a.heads_q * QImg<D>::BYTES;
+  p.nsplit = dkv_splits(a);
+  p.part = reinterpret_cast<float*>(p.kvimg + (int64_t)a.batch * p.ntk * a.heads_kv * KVImg<D>::BYTES);
   hipError_t e;
   if (p.ntq > 0) {
     pack_q_bwd_kernel<T, D><<<dim3(p.ntq, a.heads_q, a.batch), 256, 0, s>>>(p);
@@ -718,6 +1060,7 @@ template <typename T>
 hipError_t launch_t(const BwdParams& p, hipStream_t s) {
   if (p.a.head_dim == 64) return launch_d<T, 64>(p, s);
   if (p.a.head_dim == 128) return launch_d<T, 128>(p, s);
+  if (p.a.head_dim == 256) return launch_d<T, 256>(p, s);
   return hipErrorNotSupported;
 }
 
@@ -725,15 +1068,13 @@ hipError_t launch_t(const BwdParams& p, hipStream_t s) {
 
 bool prefill_bwd_mfma_supported(const goda_prefill_args& a) {
   if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16) return false;
-  return a.head_dim == 64 || a.head_dim == 128;
+  return a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256;
 }
 
 int64_t prefill_bwd_mfma_workspace_bytes(const goda_prefill_args& a) {
-  const int64_t ntq = (a.seqlen_q + kQRows - 1) / kQRows;
-  const int64_t ntk = (a.seqlen_k + kBKV - 1) / kBKV;
-  const int64_t qb = a.head_dim == 64 ? QImg<64>::BYTES : QImg<128>::BYTES;
-  const int64_t kb = a.head_dim == 64 ? KVImg<64>::BYTES : KVImg<128>::BYTES;
-  return (int64_t)a.batch * (ntq * a.heads_q * qb + ntk * a.heads_kv * kb);
+  if (a.head_dim == 64) return workspace_bytes_d<64>(a);
+  if (a.head_dim == 128) return workspace_bytes_d<128>(a);
+  return workspace_bytes_d<256>(a);
 }
 
 hipError_t launch_prefill_bwd_mfma(BwdParams p, hipStream_t s) {

@@ -42,6 +42,11 @@ struct BwdParams {
   int heads_per_wg;      // query heads per dq workgroup
   unsigned char* qimg;   // [batch][ntq][heads_q] query-tile images
   unsigned char* kvimg;  // [batch][ntk][heads_kv] key-tile images
+  // head_dim 256: the dk/dv walk over (query head, query tile) pairs is split
+  // over nsplit workgroups per key block; with nsplit > 1 they write fp32
+  // partials [nsplit][dk, dv][batch * seqlen_k][heads_kv][head_dim] here.
+  int nsplit;
+  float* part;
 };
 
 // Backward: workspace bytes and the launch (generic VALU kernels for every

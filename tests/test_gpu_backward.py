@@ -96,6 +96,18 @@ def test_backward_alibi_and_rope(dtype):
     _case(1, 40, 72, 4, 1, 256, dtype, causal=True, rope=True, seed=9)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_backward_d256_paths(dtype):
+    """head_dim 256 runs its own dk/dv kernel: one query tile (each key block
+    writes dk/dv directly), MQA with ALiBi over several key blocks (the walk is
+    split over workgroups whose partials a reduction sums), a window, and
+    Lq < Lk."""
+    _case(1, 20, 90, 4, 4, 256, dtype, causal=True, seed=11)
+    _case(2, 100, 300, 16, 1, 256, dtype, causal=True, alibi=True, seed=12)
+    _case(1, 96, 96, 4, 2, 256, dtype, causal=True, window=40, seed=13)
+    _case(1, 50, 170, 8, 2, 256, dtype, causal=True, rope=True, seed=14)
+
+
 def test_backward_rows_without_keys():
     """Lq > Lk with causal: the first Lq - Lk rows see no key; their o is 0
     and they contribute nothing (checked against the float64 brute force,
