@@ -604,26 +604,32 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
   }
   ring_barrier();
   for (int it = it0; it < it1; ++it) {
-    const bool more = it + 1 < it1;
+    // The next tile is staged into the other stage (on the last tile: this
+    // tile again, into a stage nobody reads), so the loop body is branch-free.
+    const int nx = it + 1 < it1 ? it + 1 : it;
     const int hq = hk * p.group + it / nq;
     const int q0 = (qt_lo + it % nq) * kQRows;
     const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
     const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
     const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
+    auto store_next = [&](int part) {
+      v8* dst = reinterpret_cast<v8*>(smem + ((it + 1) % 2) * QI::BYTES);
+#pragma unroll
+      for (int i = 0; i < PART; ++i) dst[tid + (part * PART + i) * NTH] = stg[i];
+      if (part == 0 && tid < 16) dst[QI::STAT + tid] = stg_stat;
+    };
 
-    if (more) load_part(it + 1, 0);
-    f32x16 s = f32x16{};
+    load_part(nx, 0);
+    // S and dP: two independent accumulation chains, interleaved.
+    f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
-    lead_schedule<KS, 4>();
-    if (more) {
-      store_part(it + 1, 0);
-      load_part(it + 1, 1);
+    for (int ks = 0; ks < KS; ++ks) {
+      s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
+      dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
     }
-    f32x16 dp = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
-    lead_schedule<KS, 4>();
+    lead_schedule<2 * KS, 4>();
+    store_next(0);
+    load_part(nx, 1);
 
     // P and dS; visibility as a range of the register's row offset
     // off = row - (q0 + 4 hi).
@@ -651,10 +657,8 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
         ds[r] = pv * (dp[r] - dl[e]);
       }
     }
-    if (more) {
-      store_part(it + 1, 1);
-      load_part(it + 1, 2);
-    }
+    store_next(1);
+    load_part(nx, 2);
     const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
@@ -662,10 +666,8 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
     }
     lead_schedule<2 * MD, 4>();
-    if (more) {
-      store_part(it + 1, 2);
-      load_part(it + 1, 3);
-    }
+    store_next(2);
+    load_part(nx, 3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
@@ -673,7 +675,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
     }
     lead_schedule<2 * MD, 4>();
-    if (more) store_part(it + 1, 3);
+    store_next(3);
     ring_barrier();
   }
 
@@ -695,33 +697,37 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       }
     return;
   }
-#pragma unroll
-  for (int md = 0; md < MD; ++md) dk[md] *= a.softmax_scale;
-  if (a.rope_k && key < g.lk) {
-    const int pos = a.rope_k_offset + key;
-#pragma unroll
-    for (int md = 0; md < MD / 2; ++md)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
-        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
-        const float x1 = dk[md][r], x2 = dk[md + MD / 2][r];
-        dk[md][r] = x1 * cs + x2 * sn;
-        dk[md + MD / 2][r] = x2 * cs - x1 * sn;
-      }
-  }
   T* krow = reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
             (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h;
   T* vrow = reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
             (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
+  auto put = [&](T* row, int md, const f32x16& x) {
 #pragma unroll
-  for (int md = 0; md < MD; ++md)
+    for (int gq = 0; gq < 4; ++gq)
+      st_vec<v4>(row + 32 * md + 8 * gq + 4 * hi, v4{(T)x[4 * gq], (T)x[4 * gq + 1], (T)x[4 * gq + 2], (T)x[4 * gq + 3]});
+  };
+  const bool rot = a.rope_k && key < g.lk;
+  const int pos = a.rope_k_offset + key;
+  // dk: one pair of head-dim blocks (md, md + MD/2: the rotation's partners)
+  // at a time, scaled and rotated back.
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int d0 = 32 * md + 8 * gq + 4 * hi;
-      st_vec<v4>(krow + d0, v4{(T)dk[md][4 * gq], (T)dk[md][4 * gq + 1], (T)dk[md][4 * gq + 2], (T)dk[md][4 * gq + 3]});
-      st_vec<v4>(vrow + d0, v4{(T)dv[md][4 * gq], (T)dv[md][4 * gq + 1], (T)dv[md][4 * gq + 2], (T)dv[md][4 * gq + 3]});
+  for (int md = 0; md < MD / 2; ++md) {
+    f32x16 x1 = dk[md] * a.softmax_scale, x2 = dk[md + MD / 2] * a.softmax_scale;
+    if (rot) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
+        const float y1 = x1[r] * cs + x2[r] * sn;
+        x2[r] = x2[r] * cs - x1[r] * sn;
+        x1[r] = y1;
+      }
     }
+    put(krow, md, x1);
+    put(krow, md + MD / 2, x2);
+  }
+#pragma unroll
+  for (int md = 0; md < MD; ++md) put(vrow, md, dv[md]);
 }
 
 // Sum of the nsplit fp32 partials of dk and dv; dk scaled and rotated back.
