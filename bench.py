@@ -333,6 +333,9 @@ def main() -> int:
         _log("bench: cfg2 backward")
         out["bwd"] = bench_backward(wl.CFG2, min(steps, 5), min(warmup, 2))
         _log(f"  {out['bwd']}")
+        _log("bench: cfg3 backward (head_dim 256)")
+        out["bwd3"] = bench_backward(wl.CFG3, min(steps, 5), min(warmup, 2))
+        _log(f"  {out['bwd3']}")
 
     cpu = None
     cpu_dec = None
@@ -448,6 +451,12 @@ def main() -> int:
                 "flops_per_launch": bw["flops"],
             },
         }
+        if "bwd3" in out:
+            b3 = out["bwd3"]
+            line["backward"]["cfg3"] = {"workload": b3["workload"], "tflops": round(b3["tflops"], 2),
+                                        "mfma_peak_frac": round(b3["tflops"] / peak_tf, 4),
+                                        "ms_per_step": round(b3["ms_per_step"], 4),
+                                        "kernel_tflops": round(b3["kernel_tflops"], 2)}
         if "cfg2" not in out and "cfg4" not in out:
             line.update(value=line["backward"]["value"], unit="TFLOP/s", ms_per_step=line["backward"]["ms_per_step"],
                         dtype="bf16", config={"workload": bw["workload"]}, roofline=line["backward"]["roofline"])
