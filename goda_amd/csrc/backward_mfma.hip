@@ -251,6 +251,19 @@ __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
   }
 }
 
+// Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
+// run LEAD MFMAs ahead (not all hoisted, which would hold 4 registers each).
+template <int NM, int LEAD>
+__device__ __forceinline__ void lead_schedule() {
+  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);
+#pragma unroll
+  for (int i = 0; i < NM - LEAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+}
+
 // Packs accumulator registers 8g..8g+7 of a 32x32 tile into an operand.
 template <typename V, typename T>
 __device__ __forceinline__ V pack8(const float* x) {
@@ -366,6 +379,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
     f32x16 s = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], bf[ks], s);
+    lead_schedule<KS, 4>();
     // Visibility as a range of the register's row offset off = row - (q0 + 4 hi).
     const int rel = q0 + 4 * hi;
     int lo_lim = -1, hi_lim = g.lq - 1 - rel;
@@ -399,6 +413,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       acc[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, acc[md]);
       acc[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, acc[md]);
     }
+    lead_schedule<2 * MD, 4>();
   };
   // B: dP for tile it.
   auto part_b_dp = [&](int it) {
@@ -406,6 +421,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
     f32x16 dp = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], bf[ks], dp);
+    lead_schedule<KS, 4>();
     return dp;
   };
   // B: dS and dK^T += Q^T dS for tile it (P of tile it from LDS).
@@ -426,6 +442,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       acc[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, acc[md]);
       acc[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, acc[md]);
     }
+    lead_schedule<2 * MD, 4>();
   };
 
   // Iteration it: A handles tile it; B computes dP of tile it and finishes
@@ -498,18 +515,6 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
 constexpr int kWavesWide = 4;
 constexpr int kWideParts = 4;
 
-// Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
-// run LEAD MFMAs ahead (not all hoisted, which would hold 4 registers each).
-template <int NM, int LEAD>
-__device__ __forceinline__ void lead_schedule() {
-  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);
-#pragma unroll
-  for (int i = 0; i < NM - LEAD; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
-}
 
 template <typename T, int D, bool ALIBI>
 __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const BwdParams p) {
@@ -887,6 +892,7 @@ __global__ void __launch_bounds__(DqShape<D>::WAVES * 64, DqShape<D>::OCC) bwd_d
         s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + l32], qf[ks], s[mt]);
         dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + l32], gf[ks], dp[mt]);
       }
+    lead_schedule<2 * KS * MT, 4>();
     // masks as ranges of the register's key offset off = key - (kvb + 4 hi)
     const int rel = kvb + 4 * hi;
     int hi_lim = g.lk - 1 - rel;
@@ -917,6 +923,7 @@ __global__ void __launch_bounds__(DqShape<D>::WAVES * 64, DqShape<D>::OCC) bwd_d
 #pragma unroll
       for (int md = 0; md < MD; ++md)
         dq[md] = mfma32(st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32], dsf[ks2], dq[md]);
+    lead_schedule<KS2 * MD, 4>();
   };
 
   if (n > 0) {
