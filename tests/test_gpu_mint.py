@@ -188,3 +188,46 @@ def test_kernels_apply_signature(cls, hkv):
     assert o.shape == (b, hq, t, d)
     o_ref = ref.attention(q.transpose(1, 2).float(), k.transpose(1, 2).float(), v.transpose(1, 2).float(), causal=True)
     assert max_err(o.transpose(1, 2), o_ref) <= 2e-2
+
+
+def test_gqa_layer_training_step_under_autocast(monkeypatch):
+    """goda trains under torch.autocast(bfloat16) by default
+    (mint/utils/device.py:15-47, mint/trainer/base.py:109): the projections
+    hand the attention bf16 q, k, v, so the layer's forward and backward run
+    on the bf16 kernels. Output and parameter gradients must agree with the
+    same layer run in fp32 (fp32 kernels) within bf16 rounding."""
+    torch.manual_seed(4)
+    e, hq, hkv, d, t = 256, 8, 2, 128, 96
+    rope = RoPE(seq_len=128, head_dim=d, rope_base_theta=10000)
+    layer = GroupedQueryAttention(hq, hkv, d, e, rope, torch.float32).to(DEV)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.05)
+        layer.q_norm.scale.normal_(0, 0.2)
+        layer.k_norm.scale.normal_(0, 0.2)
+    x = (torch.randn(2, t, e) * 0.5).to(DEV)
+    g = (torch.randn(2, t, e) * 0.5).to(DEV)
+
+    from goda_amd import ops
+
+    seen = []
+    for name in ("attention_prefill", "attention_prefill_bwd"):
+        fn = getattr(ops, name)
+        monkeypatch.setattr(ops, name, lambda *a, _fn=fn, _n=name, **kw: (seen.append((_n, a[0].dtype)), _fn(*a, **kw))[1])
+
+    def step(amp: bool):
+        layer.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+            y = layer(x)
+        (y.float() * g).sum().backward()
+        return y.detach().float(), {n: p.grad.detach().clone() for n, p in layer.named_parameters()}
+
+    y_amp, g_amp = step(True)
+    assert ("attention_prefill", torch.bfloat16) in seen and ("attention_prefill_bwd", torch.bfloat16) in seen, seen
+    seen.clear()
+    y_ref, g_ref = step(False)
+    assert ("attention_prefill_bwd", torch.float32) in seen, seen
+    assert max_err(y_amp, y_ref) <= 2e-2 * max(1.0, y_ref.abs().max().item())
+    for n, gr in g_ref.items():
+        scale = max(1.0, gr.abs().max().item())
+        assert (g_amp[n] - gr).abs().max().item() <= 3e-2 * scale, n
