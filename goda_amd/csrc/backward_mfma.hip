@@ -19,7 +19,8 @@
 //      pins the k and v operands of its keys and walks the query tiles of
 //      every head of the group (GQA reduction in the accumulators, no
 //      atomics), the tiles moving through a three-stage LDS ring. One wave
-//      of a pair computes S, P and dV, the other dP, dS and dK:
+//      of a pair computes S, dP, P and dS and hands P and dS to the other
+//      through LDS, which accumulates dV and dK one tile behind:
 //        S    [rows][keys] = Q K^T        A = Q image,   B = k (registers)
 //        dV^T [d][keys]   += dO^T P        A = dO^T image, B = P (packed S)
 //        dP   [rows][keys] = dO V^T        A = dO image,  B = v (registers)
@@ -276,20 +277,26 @@ __device__ __forceinline__ V pack8(const float* x) {
 // ---------------------------------------------------------------------------
 // 3. dk, dv
 // ---------------------------------------------------------------------------
-// Eight waves, two per SIMD, in pairs that share 32 keys: wave w < 4 ("A")
-// pins k and computes S, P and dV^T += dO^T P; wave w + 4 ("B", same SIMD)
-// pins v and computes dP and, one query tile later, dS = P (dP - delta) with
-// A's P read back from LDS, and dK^T += Q^T dS. Query tiles move through a
-// three-stage ring so that B's previous tile is still resident.
+// Eight waves, two per SIMD, in pairs that share 32 keys. Wave w < 4 ("A",
+// scores) pins the k and v operands of the keys and, per query tile, issues
+// S = Q K^T and dP = dO V^T, then computes P and dS = P (dP - delta) and
+// hands both, packed as operands, to its partner through LDS. Wave w + 4
+// ("B", gradients, same SIMD) holds the dV^T and dK^T accumulators and, one
+// tile behind, issues dV^T += dO^T P and dK^T += Q^T dS. Each iteration
+// starts with the matrix products of both waves and ends with A's VALU work:
+// a wave's VALU instructions do not issue while the other wave of its SIMD
+// has matrix instructions waiting, so no VALU work sits between B's products.
+// Query tiles move through a three-stage ring (A reads tile it, B tile it-1,
+// tile it+1 is being stored); the P / dS exchange is double-buffered.
 constexpr int kWavesKv = 8;
 constexpr int kKvStages = 3;
 
 template <int D>
 struct DkvSmem {
   static constexpr int64_t RING = kKvStages * QImg<D>::BYTES;
-  // P exchange: [parity][pair][register group][lane] f32x4
-  static constexpr int64_t PBUF = 2 * 4 * 4 * 64 * 16;
-  static constexpr int64_t BYTES = RING + PBUF;
+  // operand exchange: [parity][pair][P0, P1, dS0, dS1][lane] 16-byte chunks
+  static constexpr int64_t XBUF = 2 * 4 * 4 * 64 * 16;
+  static constexpr int64_t BYTES = RING + XBUF;
 };
 
 template <typename T, int D, bool ALIBI>
@@ -303,7 +310,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   constexpr int LOADS = 4 * QI::CH / (kWavesKv * 64);
   static_assert(4 * QI::CH % (kWavesKv * 64) == 0, "tile must split over the waves");
   extern __shared__ __align__(16) unsigned char smem[];
-  f32x4* pbuf = reinterpret_cast<f32x4*>(smem + DkvSmem<D>::RING);
+  v8* xbuf = reinterpret_cast<v8*>(smem + DkvSmem<D>::RING);
 
   const goda_prefill_args& a = p.a;
   const int b = blockIdx.z, hk = blockIdx.y;
@@ -321,24 +328,6 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   const int key = kw0 + l32;
   const int diag = g.lk - g.lq;
   const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
-
-  // B operand of this wave's 32 keys: k (A) or v (B), from the key images.
-  v8 bf[KS];
-  if (kw0 < g.lk) {
-    const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
-    const int base = role_b ? KI::VA : KI::KA;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) bf[ks] = img[base + (2 * ks + hi) * kBKV + l32];
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) bf[ks] = v8{};
-  }
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(bf[ks]));
-
-  f32x16 acc[MD];  // dV^T (A) or dK^T (B)
-#pragma unroll
-  for (int md = 0; md < MD; ++md) acc[md] = f32x16{};
 
   // Query tiles that can see a key of this workgroup.
   const int kv_last = min(kv0 + 128, g.lk) - 1;
@@ -367,139 +356,146 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
     if (tid < 16) dst[QI::STAT + tid] = stg_stat;
   };
   auto stage = [&](int it) { return reinterpret_cast<const v8*>(smem + (it % kKvStages) * QI::BYTES); };
+  auto xchg = [&](int it, int c) -> v8& { return xbuf[(((it & 1) * 4 + pair) * 4 + c) * 64 + lane]; };
 
-  const float c = p.scale_log2;
-  // A: S, P (to LDS), dV^T += dO^T P for tile it.
-  auto part_a = [&](int it) {
-    const int hq = hk * p.group + it / nq;
-    const int q0 = (qt_lo + it % nq) * kQRows;
-    const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
-    const v8* st = stage(it);
-    const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
-    f32x16 s = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], bf[ks], s);
-    lead_schedule<KS, 4>();
-    // Visibility as a range of the register's row offset off = row - (q0 + 4 hi).
-    const int rel = q0 + 4 * hi;
-    int lo_lim = -1, hi_lim = g.lq - 1 - rel;
-    if (a.causal) lo_lim = key - diag - rel;
-    if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
-    const bool key_ok = key < g.lk;
-    const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27;
-    const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
-    f32x4 pr4[4];
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * gq + e;
-        const int off = 8 * gq + e;
-        float t = s[r] * c;
-        if (ALIBI) t += base - slope2 * (float)off;
-        float pv = fast_exp2(t - l2[e]);
-        if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
-        pr4[gq][e] = pv;
-      }
-      pbuf[((it & 1) * 4 + pair) * 4 * 64 + gq * 64 + lane] = pr4[gq];
-    }
-    float pr[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) pr[r] = pr4[r >> 2][r & 3];
-    const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
-#pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      acc[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, acc[md]);
-      acc[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, acc[md]);
-    }
-    lead_schedule<2 * MD, 4>();
-  };
-  // B: dP for tile it.
-  auto part_b_dp = [&](int it) {
-    const v8* st = stage(it);
-    f32x16 dp = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], bf[ks], dp);
-    lead_schedule<KS, 4>();
-    return dp;
-  };
-  // B: dS and dK^T += Q^T dS for tile it (P of tile it from LDS).
-  auto part_b_dk = [&](int it, const f32x16& dp) {
-    const v8* st = stage(it);
-    const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
-    float ds[16];
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4 pv = pbuf[((it & 1) * 4 + pair) * 4 * 64 + gq * 64 + lane];
-      const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ds[4 * gq + e] = pv[e] * (dp[4 * gq + e] - dl[e]);
-    }
-    const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
-#pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      acc[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, acc[md]);
-      acc[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, acc[md]);
-    }
-    lead_schedule<2 * MD, 4>();
-  };
-
-  // Iteration it: A handles tile it; B computes dP of tile it and finishes
-  // tile it - 1. Stages in use: (it - 1) % 3 and it % 3; tile it + 1 is
-  // loaded at the start and stored at the end into the third stage.
   if (n > 0) {
     tile_load(0);
     tile_store(0);
   }
-  f32x16 dp_prev = f32x16{};
+
+  if (!role_b) {
+    // ---- A: scores --------------------------------------------------------
+    v8 kf[KS], vf[KS];
+    if (kw0 < g.lk) {
+      const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + l32];
+        vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + l32];
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = vf[ks] = v8{};
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      asm volatile("" : "+v"(kf[ks]));
+      asm volatile("" : "+v"(vf[ks]));
+    }
+    const float c = p.scale_log2;
+    const bool key_ok = key < g.lk;
+    for (int it = 0; it <= n; ++it) {
+      ring_barrier();
+      if (it + 1 < n) tile_load(it + 1);
+      if (it < n) {
+        const int hq = hk * p.group + it / nq;
+        const int q0 = (qt_lo + it % nq) * kQRows;
+        const v8* st = stage(it);
+        const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
+        // S [rows][keys] and dP: two interleaved accumulation chains.
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
+          dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
+        }
+        lead_schedule<2 * KS, 4>();
+        // P and dS; visibility as a range of the register's row offset
+        // off = row - (q0 + 4 hi).
+        const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
+        const int rel = q0 + 4 * hi;
+        int lo_lim = -1, hi_lim = g.lq - 1 - rel;
+        if (a.causal) lo_lim = key - diag - rel;
+        if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
+        const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27;
+        const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
+        float pr[16], ds[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
+          const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * gq + e;
+            const int off = 8 * gq + e;
+            float t = s[r] * c;
+            if (ALIBI) t += base - slope2 * (float)off;
+            float pv = fast_exp2(t - l2[e]);
+            if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+            pr[r] = pv;
+            ds[r] = pv * (dp[r] - dl[e]);
+          }
+        }
+        xchg(it, 0) = pack8<v8, T>(pr);
+        xchg(it, 1) = pack8<v8, T>(pr + 8);
+        xchg(it, 2) = pack8<v8, T>(ds);
+        xchg(it, 3) = pack8<v8, T>(ds + 8);
+      }
+      if (it + 1 < n) tile_store(it + 1);
+    }
+    return;
+  }
+
+  // ---- B: gradients ---------------------------------------------------------
+  f32x16 dv[MD], dk[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) dv[md] = dk[md] = f32x16{};
   for (int it = 0; it <= n; ++it) {
     ring_barrier();
     if (it + 1 < n) tile_load(it + 1);
-    if (!role_b) {
-      if (it < n) part_a(it);
-    } else {
-      f32x16 dp_cur = f32x16{};
-      if (it < n) dp_cur = part_b_dp(it);
-      if (it > 0) part_b_dk(it - 1, dp_prev);
-      dp_prev = dp_cur;
+    if (it > 0) {
+      const v8* st = stage(it - 1);
+      const v8 p0 = xchg(it - 1, 0), p1 = xchg(it - 1, 1);
+      const v8 d0 = xchg(it - 1, 2), d1 = xchg(it - 1, 3);
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+        dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], p0, dv[md]);
+        dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
+      }
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+        dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], p1, dv[md]);
+        dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
+      }
+      lead_schedule<4 * MD, 4>();
     }
     if (it + 1 < n) tile_store(it + 1);
   }
 
   // ---- epilogue: lane l32 owns key row `key`; register (md, r) is head-dim
-  // 32 md + 8 (r/4) + 4 hi + r%4. A writes dV, B writes dK.
+  // 32 md + 8 (r/4) + 4 hi + r%4.
   if (key >= kend) return;
-  if (role_b) {
+  T* krow = reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
+            (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h;
+  T* vrow = reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
+            (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
+  auto put = [&](T* row, int md, const f32x16& x) {
 #pragma unroll
-    for (int md = 0; md < MD; ++md) acc[md] *= a.softmax_scale;
-    if (a.rope_k && key < g.lk) {
-      // transpose of the rotation: pairs (d, d + D/2) are blocks md, md + MD/2
-      const int pos = a.rope_k_offset + key;
+    for (int gq = 0; gq < 4; ++gq)
+      st_vec<v4>(row + 32 * md + 8 * gq + 4 * hi, v4{(T)x[4 * gq], (T)x[4 * gq + 1], (T)x[4 * gq + 2], (T)x[4 * gq + 3]});
+  };
+  const bool rot = a.rope_k && key < g.lk;
+  const int pos = a.rope_k_offset + key;
+  // dk: pairs of head-dim blocks (md, md + MD/2: the rotation's partners),
+  // scaled and rotated back.
 #pragma unroll
-      for (int md = 0; md < MD / 2; ++md)
+  for (int md = 0; md < MD / 2; ++md) {
+    f32x16 x1 = dk[md] * a.softmax_scale, x2 = dk[md + MD / 2] * a.softmax_scale;
+    if (rot) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
-          const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
-          const float x1 = acc[md][r], x2 = acc[md + MD / 2][r];
-          acc[md][r] = x1 * cs + x2 * sn;
-          acc[md + MD / 2][r] = x2 * cs - x1 * sn;
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * md + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float cs = a.rope_cos[(int64_t)pos * (D / 2) + d], sn = a.rope_sin[(int64_t)pos * (D / 2) + d];
+        const float y1 = x1[r] * cs + x2[r] * sn;
+        x2[r] = x2[r] * cs - x1[r] * sn;
+        x1[r] = y1;
+      }
     }
+    put(krow, md, x1);
+    put(krow, md + MD / 2, x2);
   }
-  T* row = role_b ? reinterpret_cast<T*>(p.g.dk) + (varlen ? 0 : (int64_t)b * p.g.dk_stride_b) +
-                        (g.k_row0 + key) * p.g.dk_stride_t + (int64_t)hk * p.g.dk_stride_h
-                  : reinterpret_cast<T*>(p.g.dv) + (varlen ? 0 : (int64_t)b * p.g.dv_stride_b) +
-                        (g.k_row0 + key) * p.g.dv_stride_t + (int64_t)hk * p.g.dv_stride_h;
 #pragma unroll
-  for (int md = 0; md < MD; ++md)
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int d0 = 32 * md + 8 * gq + 4 * hi;
-      const v4 x4 = {(T)acc[md][4 * gq], (T)acc[md][4 * gq + 1], (T)acc[md][4 * gq + 2], (T)acc[md][4 * gq + 3]};
-      st_vec<v4>(row + d0, x4);
-    }
+  for (int md = 0; md < MD; ++md) put(vrow, md, dv[md]);
 }
 
 // ---------------------------------------------------------------------------
