@@ -60,10 +60,12 @@ struct TileGeom {
   static_assert((K_CHUNKS + V_CHUNKS) % (64 * WAVES) == 0, "tile must split evenly over the waves");
 };
 constexpr int kStages = 3;  // LDS ring: tiles j, j+1 read, tile j+2 written
-// Move each tile in two halves through half the staging registers (register
-// relief for D = 256, whose two-waves-per-SIMD form is at the limit).
+// Move each tile in two halves through half the staging registers: register
+// relief for D = 256 (whose two-waves-per-SIMD form is at the limit), and at
+// D = 128 half of the LDS stores move from the end of the interval, where
+// the ring barrier waits for them, to its middle (cfg2 +2-4%).
 template <int D>
-constexpr bool kSplitStaging = D >= 256;
+constexpr bool kSplitStaging = D >= 128;
 
 // Index of workspace tile j of sequence b, KV head hk.
 __device__ __forceinline__ int64_t ws_tile(int b, int j, int hk, int ntiles, int hkv) {
