@@ -25,12 +25,17 @@
 //      compiler waits for ALL LDS reads before every MFMA operand use.)
 //
 // Per wave and KV tile (32x32x16 MFMA, 32*NT query rows of one head):
-//   S^T[kv][q] = K'[kv][d] . Q^T[d][q]     A = K' (LDS), B = Q^T (registers)
+//   S^T[kv][q] = K'[kv][d] . Q^T[d][q] - m[q] + bias[kv][q]
+//                                          A = K' (LDS), B = Q^T (registers)
 //   O^T[d][q] += V^T[d][kv] . P^T[kv][q]   A = V^T (LDS), B = P^T (registers)
+// Q^T holds q * scale * log2(e) and the accumulators start at the row's
+// reference max m (negated) plus the ALiBi bias, so the scores leave the
+// MFMA as the exponents of P: the softmax spends no VALU instruction on
+// scaling, biasing or shifting them (the VALU work of a wave does not issue
+// while the other wave of its SIMD has matrix instructions waiting, so every
+// VALU instruction of the softmax lengthens the interval).
 // Every query row lives in one lane pair (l, l^32), so the row max needs one
-// permlane32 swap and any rescale is lane-local. The loop is software
-// pipelined: the MFMAs of S(j+1) are issued next to the exp / convert /
-// row-sum VALU work on S(j); P(j)V(j) follows.
+// permlane32 swap and any rescale is lane-local.
 // Rescaling is lazy: a row's reference max only moves (and its O and l are
 // rescaled) when the tile max exceeds it by more than kRescaleThresh (log2
 // units), so O is untouched by the VALU on almost every tile. The result is
@@ -267,6 +272,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   constexpr int MD = D / 32;     // 32-wide head-dim tiles of O^T
   constexpr int KS2 = BKV / 16;  // k-steps of PV
   static_assert(MT >= 1, "tile shape");
+  static_assert(WAVES == 8, "two waves per SIMD, in two groups half an interval apart");
 
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -317,8 +323,10 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         const T* qr = qbase + (g.q_row0 + qi) * a.q_stride_t;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = ld_vec<v8>(qr + 16 * ks + 8 * hi);
-        if (a.q_norm_weight || a.rope_q) {
-          // fp32 round trip: fused QK-RMSNorm, then RoPE, one rounding.
+        {
+          // fp32 round trip: fused QK-RMSNorm, then RoPE, then the softmax
+          // scale in log2 units (scores come out of the MFMA ready for exp2),
+          // one rounding.
           float xf[KS][8];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks)
@@ -360,7 +368,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qf[nt][ks][e] = (T)xf[ks][e];
+            for (int e = 0; e < 8; ++e) qf[nt][ks][e] = (T)(xf[ks][e] * p.scale_log2);
         }
       } else {
 #pragma unroll
@@ -435,12 +443,31 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 
   // This lane's K' operand for (ks, mt) is chunk (2ks + hi)*BKV + 32mt + l32;
   // its V^T operand for (ks2, md) is chunk (2ks2 + hi)*D + 32md + l32.
+  // S^T(j) in log2 units relative to the row's current reference max: the
+  // accumulators start at -m (plus the ALiBi bias slope*(kv - i) of each
+  // register), so a score leaves the MFMA as the exponent of its P.
   auto qk = [&](int j, f32x16 (&s)[MT][NT]) {
     const v8* kp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES) + hi * BKV + l32;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int nt = 0; nt < NT; ++nt) {
+      const float m0 = (m_run[nt] == kNegInf) ? 0.f : -m_run[nt];
+      if (ALIBI) {
+        const int iabs = diag + wrow0 + 32 * nt + l32;
+        float bg = m0 + slope2 * (float)(j * BKV + 4 * hi - iabs);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) s[mt][nt] = f32x16{};
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if ((r & 3) == 0 && (mt | r) != 0) bg += alibi_s8;
+            s[mt][nt][r] = (r & 3) == 0 ? bg : (r & 3) == 1 ? bg + alibi_s1 : (r & 3) == 2 ? bg + alibi_s2 : bg + alibi_s3;
+          }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[mt][nt][r] = m0;
+      }
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -452,19 +479,17 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   };
 
   // ---- softmax half of a step: scores s of tile j -> probabilities pf --------------
+  // The scores arrive as exponents relative to the reference max the row had
+  // when S(j) was issued (the same m_run as now: nothing updates it between
+  // an S tile's products and its softmax).
   auto vpart = [&](int j, f32x16 (&s)[MT][NT], v8 (&pf)[NT][KS2]) {
     const int kvb = j * BKV;
     const bool need_mask = (kvb + BKV > g.lk) || (a.causal && kvb + BKV - 1 > diag + wrow0) ||
                            (use_window && kvb < diag + wrow0 + 32 * NT - 1 - a.window_left);
-    if (ALIBI || need_mask) {
+    if (need_mask) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int iabs = diag + wrow0 + 32 * nt + l32;
-        // ALiBi: slope * (kv - iabs). Registers come in groups of 4
-        // consecutive keys, groups 8 keys apart: a group base advanced by
-        // 8 slope per group, plus {0, 1, 2, 3} slope inside the group (four
-        // loop-invariant values instead of one per register).
-        float bg = ALIBI ? slope2 * (float)(kvb + 4 * hi - iabs) : 0.f;
         // Visibility as a range of the register's key offset
         // off = kv - (kvb + 4 hi), a compile-time constant per register:
         // lo_lim <= off <= hi_lim (no per-register key index is formed).
@@ -477,21 +502,12 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int off = 32 * mt + 8 * (r >> 2) + (r & 3);
-            float t = s[mt][nt][r];
-            if (ALIBI) {
-              if ((r & 3) == 0 && (mt | r) != 0) bg += alibi_s8;
-              t = fmaf(t, c, bg);
-              if ((r & 3) == 1) t += alibi_s1;
-              if ((r & 3) == 2) t += alibi_s2;
-              if ((r & 3) == 3) t += alibi_s3;
-            }
-            if (need_mask) t = (off >= lo_lim && off <= hi_lim) ? t : kNegInf;
-            s[mt][nt][r] = t;
+            s[mt][nt][r] = (off >= lo_lim && off <= hi_lim) ? s[mt][nt][r] : kNegInf;
           }
       }
     }
-    // row max and lazy rescale
-    float mtile[NT];
+    // row max (absolute, log2 units) and lazy rescale
+    float mtile[NT], mq[NT];
     bool grow = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -500,25 +516,31 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; r += 2) mx = max3f(mx, s[mt][nt][r], s[mt][nt][r + 1]);
-      mx = half_max(mx);
-      mtile[nt] = ALIBI ? mx : mx * c;
+      mq[nt] = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];  // shift the scores carry
+      mtile[nt] = half_max(mx) + mq[nt];
       grow = grow || (mtile[nt] > m_run[nt] + kRescaleThresh);
     }
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      // the max moved: rescale O and l, and bring the scores to the new
+      // reference (rare: the reference only moves by more than the threshold)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const float mn = fmaxf(m_run[nt], mtile[nt]);
         const float alpha = (m_run[nt] == kNegInf) ? 0.f : fast_exp2(m_run[nt] - mn);
+        const float shift = (mn == kNegInf) ? 0.f : mn - mq[nt];
         m_run[nt] = mn;
         l_run[nt] *= alpha;
 #pragma unroll
         for (int md = 0; md < MD; ++md) oacc[md][nt] *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[mt][nt][r] -= shift;
       }
     }
     // probabilities (rounded to the operand type) and their row sums
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float m_use = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];
       float lsum = l_run[nt];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -526,10 +548,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         for (int h = 0; h < 2; ++h) {
           v8 pv;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = s[mt][nt][8 * h + e];
-            pv[e] = (T)(ALIBI ? fast_exp2(x - m_use) : fast_exp2(fmaf(x, c, -m_use)));
-          }
+          for (int e = 0; e < 8; ++e) pv[e] = (T)fast_exp2(s[mt][nt][8 * h + e]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) lsum = dot2_ones(pv, i, lsum);
           pf[nt][2 * mt + h] = pv;
@@ -609,7 +628,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     qk(j_lo, s_a);
   }
 
-  if constexpr (WAVES == 8) {
+  {
     // Two waves share each SIMD (waves w and w+4). They run the same
     // sequence of tiles half an interval apart, so one wave's MFMA work
     // (P(j)V(j) and S(j+1)) overlaps the other's softmax:
@@ -630,23 +649,6 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         if (j + 1 < j_hi) vpart(j + 1, s_a, pf);
       }
       ring_end(j);
-    }
-  } else {
-    // One wave per SIMD: overlap inside the wave instead. The MFMAs of
-    // S(j+1) are issued in the same basic block as the softmax VALU work on
-    // S(j) (unconditionally: the last step recomputes tile j and drops it).
-    f32x16 s_b[MT][NT];
-    auto step = [&](int j, f32x16 (&s_in)[MT][NT], f32x16 (&s_out)[MT][NT]) {
-      ring_begin(j);
-      qk(j + 1 < j_hi ? j + 1 : j, s_out);
-      vpart(j, s_in, pf);
-      pv_mfma(j, pf);
-      ring_end(j);
-    };
-    // Unrolled by two so the score buffers alternate without register copies.
-    for (int j = j_lo; j < j_hi; j += 2) {
-      step(j, s_a, s_b);
-      if (j + 1 < j_hi) step(j + 1, s_b, s_a);
     }
   }
 
@@ -684,10 +686,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 // host side
 // ---------------------------------------------------------------------------
 // Tile shape per head dim: keys per tile, 32-row query tiles per wave, waves
-// per workgroup (8 = two per SIMD, so one wave's MFMAs overlap the other's
-// softmax; the 4-wave form, one per SIMD, serves a wave that needs more than
-// half the register file). D = 256 fits two waves per SIMD with 32-key tiles
-// (measured 1.5x the one-wave form on cfg3/cfg5).
+// per workgroup (8 = two per SIMD, in two groups half an interval apart).
+// D = 256 fits two waves per SIMD with 32-key tiles (measured 1.5x a form
+// with one wave per SIMD on cfg3/cfg5).
 template <int D>
 struct Config;
 template <>
