@@ -183,7 +183,8 @@ __device__ __forceinline__ const DecodeParams& reload_params() {
   asm volatile("" : "+s"(pp));
   return *pp;
 #else
-  return *static_cast<const DecodeParams*>(nullptr);  // host pass: never executed
+  static const DecodeParams unused{};  // host pass: never executed
+  return unused;
 #endif
 }
 

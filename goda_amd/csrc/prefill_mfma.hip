@@ -404,7 +404,6 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     m_run[nt] = kNegInf;
     l_run[nt] = 0.f;
   }
-  const float c = p.scale_log2;
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
   const float alibi_s1 = slope2, alibi_s2 = 2.f * slope2, alibi_s3 = 3.f * slope2, alibi_s8 = 8.f * slope2;
 
