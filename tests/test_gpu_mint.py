@@ -8,6 +8,7 @@ import math
 import pytest
 import torch
 
+from goda_amd import ops
 from goda_amd import workloads as wl
 from goda_amd.kernels_ import FlashAttentionGQAKernel, FlashAttentionMQAKernel
 from goda_amd.mint.kvcache import KVCache
@@ -231,3 +232,22 @@ def test_gqa_layer_training_step_under_autocast(monkeypatch):
     for n, gr in g_ref.items():
         scale = max(1.0, gr.abs().max().item())
         assert (g_amp[n] - gr).abs().max().item() <= 3e-2 * scale, n
+
+
+def test_kvcache_head_major_storage_decodes_like_contiguous():
+    """KVCache keeps goda's tensor shape [B, Lmax, Hkv, D] over head-major
+    storage; a decode over its tensors equals one over a contiguous copy."""
+    b, lmax, hkv, hq, d = 3, 96, 2, 8, 128
+    cache = KVCache(max_batch_size=b, max_seq_len=lmax, n_kv_heads=hkv, head_dim=d, dtype=torch.bfloat16, device=DEV)
+    assert cache.k_cache.shape == (b, lmax, hkv, d) and cache.k_cache.stride(1) == d
+    lens = [5, 40, 96]
+    k = _rand((b, lmax, hkv, d), torch.bfloat16, 60).to(DEV)
+    v = _rand((b, lmax, hkv, d), torch.bfloat16, 61).to(DEV)
+    cache.append(k, v)
+    cache.cache_seqlens.copy_(torch.tensor(lens, dtype=torch.int32))
+    assert torch.equal(cache.k_cache, k) and torch.equal(cache.v_cache, v)
+    q = _rand((b, hq, d), torch.bfloat16, 62).to(DEV)
+    kc, vc, seqlens = cache.get_cache_tensors()
+    o1 = ops.attention_decode(q, kc, vc, seqlens)
+    o2 = ops.attention_decode(q, kc.contiguous(), vc.contiguous(), seqlens)
+    assert torch.equal(o1, o2)
