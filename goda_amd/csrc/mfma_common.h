@@ -18,6 +18,14 @@ struct Vec<f16> {
   typedef f16x8 v8;
   typedef f16x4 v4;
 };
+template <>
+struct Vec<float> {
+  typedef f32x8 v8;
+  typedef f32x4 v4;
+};
+// Matrix instructions issued per mfma32() call (a 32x32 tile, 16 steps of K).
+template <typename T>
+constexpr int kMfmaPerStep = sizeof(T) == 4 ? 8 : 1;
 
 // 32x32 MFMA accumulator layout (gfx9 family): lane l, register r holds row
 // 8*(r/4) + 4*(l/32) + r%4, column l%32; the K dimension of the A and B

@@ -56,11 +56,12 @@ namespace {
 constexpr float kRescaleThresh = 8.0f;  // log2 units: P entries stay <= 2^8
 
 
-template <int D, int BKV, int WAVES>
+template <typename T, int D, int BKV, int WAVES>
 struct TileGeom {
+  static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);  // bytes per 8-element chunk
   static constexpr int K_CHUNKS = D / 8 * BKV;  // 16-byte chunks of the K' image
   static constexpr int V_CHUNKS = BKV / 8 * D;
-  static constexpr int BYTES = (K_CHUNKS + V_CHUNKS) * 16;
+  static constexpr int BYTES = (K_CHUNKS + V_CHUNKS) * CHB;
   static constexpr int LOADS_PER_LANE = (K_CHUNKS + V_CHUNKS) / (64 * WAVES);  // 16-byte loads
   static_assert((K_CHUNKS + V_CHUNKS) % (64 * WAVES) == 0, "tile must split evenly over the waves");
 };
@@ -84,7 +85,7 @@ __device__ __forceinline__ int64_t ws_tile(int b, int j, int hk, int ntiles, int
 template <typename T, int D, int BKV>
 __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
   typedef typename Vec<T>::v8 v8;
-  typedef TileGeom<D, BKV, 1> TG;
+  typedef TileGeom<T, D, BKV, 1> TG;
   const goda_prefill_args& a = p.a;
   const int j = blockIdx.x;
   const int hk = blockIdx.y;
@@ -97,7 +98,7 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
   unsigned char* tile = reinterpret_cast<unsigned char*>(a.workspace) +
                         ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES;
   v8* kimg = reinterpret_cast<v8*>(tile);
-  v8* vimg = reinterpret_cast<v8*>(tile + TG::K_CHUNKS * 16);
+  v8* vimg = reinterpret_cast<v8*>(tile + TG::K_CHUNKS * TG::CHB);
 
   const T* kbase = reinterpret_cast<const T*>(a.k) +
                    (a.cu_seqlens_k ? 0 : (int64_t)b * a.k_stride_b) + (int64_t)hk * a.k_stride_h;
@@ -255,6 +256,7 @@ __device__ __forceinline__ float dot2_ones(bf16x8 p, int i, float acc) {
   const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
   return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
 }
+__device__ __forceinline__ float dot2_ones(f32x8 p, int i, float acc) { return acc + p[2 * i] + p[2 * i + 1]; }
 __device__ __forceinline__ float dot2_ones(f16x8 p, int i, float acc) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const h2 v = {p[2 * i], p[2 * i + 1]};
@@ -266,7 +268,7 @@ template <typename T, int D, int BKV, int NT, int WAVES, bool ALIBI>
 __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const PrefillParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
-  typedef TileGeom<D, BKV, WAVES> TG;
+  typedef TileGeom<T, D, BKV, WAVES> TG;
   constexpr int MT = BKV / 32;   // 32-key row tiles of S^T
   constexpr int KS = D / 16;     // k-steps of QK^T
   constexpr int MD = D / 32;     // 32-wide head-dim tiles of O^T
@@ -559,7 +561,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 
   // ---- O^T += V^T P^T for tile j ----------------------------------------------------
   auto pv_mfma = [&](int j, const v8 (&pf)[NT][KS2]) {
-    const v8* vp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES + TG::K_CHUNKS * 16) +
+    const v8* vp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES + TG::K_CHUNKS * TG::CHB) +
                    hi * D + l32;
 #pragma unroll
     for (int ks2 = 0; ks2 < KS2; ++ks2)
@@ -579,8 +581,10 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   auto mphase = [&](int j, const v8 (&pf)[NT][KS2], f32x16 (&s)[MT][NT]) {
     pv_mfma(j, pf);
     qk(j + 1 < j_hi ? j + 1 : j, s);
-    constexpr int kMfma = KS2 * MD * NT + KS * MT * NT;
-    constexpr int kReads = KS2 * MD + KS * MT;
+    // counted in instructions: an fp32 step is 8 MFMAs and its 32-byte
+    // operand two 16-byte LDS reads
+    constexpr int kMfma = (KS2 * MD * NT + KS * MT * NT) * kMfmaPerStep<T>;
+    constexpr int kReads = (KS2 * MD + KS * MT) * TG::CHB / 16;
     constexpr int kLead = 4;
     static_assert(kReads > kLead, "phase too short");
     __builtin_amdgcn_sched_group_barrier(0x100, kLead, 0);
@@ -688,22 +692,28 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 // per workgroup (8 = two per SIMD, in two groups half an interval apart).
 // D = 256 fits two waves per SIMD with 32-key tiles (measured 1.5x a form
 // with one wave per SIMD on cfg3/cfg5).
-template <int D>
+// fp32 operands (D <= 128) double the tile bytes: D = 128 takes 32-key tiles
+// so three LDS stages still fit.
+template <typename T, int D>
 struct Config;
-template <>
-struct Config<64> {
+template <typename T>
+struct Config<T, 64> {
   static constexpr int BKV = 64, NT = 1, WAVES = 8;
 };
-template <>
-struct Config<128> {
-  static constexpr int BKV = 64, NT = 1, WAVES = 8;
+template <typename T>
+struct Config<T, 128> {
+  static constexpr int BKV = sizeof(T) == 4 ? 32 : 64, NT = 1, WAVES = 8;
 };
-template <>
-struct Config<256> {
+template <typename T>
+struct Config<T, 256> {
+  static_assert(sizeof(T) == 2, "fp32 at head_dim 256 takes the generic kernel");
   static constexpr int BKV = 32, NT = 1, WAVES = 8;
 };
 
-int kv_tile_for(int d) { return d >= 256 ? Config<256>::BKV : d >= 128 ? Config<128>::BKV : Config<64>::BKV; }
+int kv_tile_for(int d, int dtype) {
+  if (dtype == GODA_DTYPE_F32) return d >= 128 ? Config<float, 128>::BKV : Config<float, 64>::BKV;
+  return d >= 256 ? Config<bf16, 256>::BKV : d >= 128 ? Config<bf16, 128>::BKV : Config<bf16, 64>::BKV;
+}
 
 int gcd_int(int x, int y) {
   while (y) {
@@ -716,7 +726,7 @@ int gcd_int(int x, int y) {
 
 template <typename T, int D, bool ALIBI>
 hipError_t launch_attn(PrefillParams p, hipStream_t s) {
-  typedef Config<D> C;
+  typedef Config<T, D> C;
   const goda_prefill_args& a = p.a;
   const int hg = gcd_int(p.group, C::WAVES);
   p.heads_per_wg = hg;
@@ -725,7 +735,7 @@ hipError_t launch_attn(PrefillParams p, hipStream_t s) {
   const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / hg);
   if (nblk <= 0) return hipSuccess;
   if (nblk > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t lds = (size_t)kStages * TileGeom<D, C::BKV, C::WAVES>::BYTES;
+  const size_t lds = (size_t)kStages * TileGeom<T, D, C::BKV, C::WAVES>::BYTES;
   auto kern = prefill_fa_kernel<T, D, C::BKV, C::NT, C::WAVES, ALIBI>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
@@ -738,7 +748,7 @@ hipError_t launch_attn(PrefillParams p, hipStream_t s) {
 
 template <typename T, int D>
 hipError_t launch_d(PrefillParams p, hipStream_t s) {
-  constexpr int BKV = Config<D>::BKV;
+  constexpr int BKV = Config<T, D>::BKV;
   const goda_prefill_args& a = p.a;
   p.kv_tile = BKV;
   p.ntiles_k = (a.seqlen_k + BKV - 1) / BKV;
@@ -760,7 +770,8 @@ hipError_t launch_t(const PrefillParams& p, hipStream_t s) {
     case 128:
       return launch_d<T, 128>(p, s);
     case 256:
-      return launch_d<T, 256>(p, s);
+      if constexpr (sizeof(T) == 2) return launch_d<T, 256>(p, s);
+      return hipErrorNotSupported;
     default:
       return hipErrorNotSupported;
   }
@@ -769,19 +780,22 @@ hipError_t launch_t(const PrefillParams& p, hipStream_t s) {
 }  // namespace
 
 bool prefill_mfma_supported(const goda_prefill_args& a) {
+  if (a.dtype == GODA_DTYPE_F32) return a.head_dim == 64 || a.head_dim == 128;
   if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16) return false;
   return a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256;
 }
 
 int64_t prefill_mfma_workspace_bytes(const goda_prefill_args& a) {
-  const int bkv = kv_tile_for(a.head_dim);
+  const int bkv = kv_tile_for(a.head_dim, a.dtype);
   const int64_t ntiles = (a.seqlen_k + bkv - 1) / bkv;
-  return 2 * (int64_t)a.batch * ntiles * a.heads_kv * bkv * a.head_dim * 2;
+  const int64_t elem = a.dtype == GODA_DTYPE_F32 ? 4 : 2;
+  return 2 * (int64_t)a.batch * ntiles * a.heads_kv * bkv * a.head_dim * elem;
 }
 
 hipError_t launch_prefill_mfma(const PrefillParams& p, hipStream_t s) {
   if (p.a.dtype == GODA_DTYPE_BF16) return launch_t<bf16>(p, s);
   if (p.a.dtype == GODA_DTYPE_F16) return launch_t<f16>(p, s);
+  if (p.a.dtype == GODA_DTYPE_F32) return launch_t<float>(p, s);
   return hipErrorNotSupported;
 }
 
