@@ -54,27 +54,32 @@ constexpr int kQRows = 32;   // rows per query tile
 constexpr int kBKV = 32;     // keys per key tile
 // dq workgroup: two waves per SIMD, or one at head_dim 256 (q and dO operands
 // plus the dQ^T accumulator take ~350 registers there).
-template <int D>
+template <typename T, int D>
 struct DqShape {
-  static constexpr int WAVES = D >= 256 ? 4 : 8;
-  static constexpr int OCC = D >= 256 ? 1 : 2;
+  static constexpr bool WIDE = D >= 256 || sizeof(T) == 4;
+  static constexpr int WAVES = WIDE ? 4 : 8;
+  static constexpr int OCC = WIDE ? 1 : 2;
 };
 
-template <int D>
+// Images are counted in 8-element chunks (16 bytes, or 32 for fp32).
+template <typename T, int D>
 struct QImg {
-  static constexpr int CH = D / 8 * kQRows;  // 16-byte chunks of one image
+  static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);
+  static constexpr int CH = D / 8 * kQRows;  // chunks of one image
   static constexpr int QA = 0, GA = CH, QT = 2 * CH, GT = 3 * CH;
-  static constexpr int STAT = 4 * CH;        // lse2[32] then delta[32]: 16 chunks
-  static constexpr int CHUNKS = 4 * CH + 16;
-  static constexpr int64_t BYTES = (int64_t)CHUNKS * 16;
+  static constexpr int STAT = 4 * CH;        // lse2[32] then delta[32]: 256 bytes
+  static constexpr int STAT_CH = 256 / CHB;
+  static constexpr int CHUNKS = 4 * CH + STAT_CH;
+  static constexpr int64_t BYTES = (int64_t)CHUNKS * CHB;
 };
 
-template <int D>
+template <typename T, int D>
 struct KVImg {
+  static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);
   static constexpr int CH = D / 8 * kBKV;
   static constexpr int KA = 0, VA = CH, KT = 2 * CH;
   static constexpr int CHUNKS = 3 * CH;
-  static constexpr int64_t BYTES = (int64_t)CHUNKS * 16;
+  static constexpr int64_t BYTES = (int64_t)CHUNKS * CHB;
 };
 
 __device__ __forceinline__ int64_t q_tile_index(int b, int qt, int hq, int ntq, int heads_q) {
@@ -96,7 +101,7 @@ __device__ __forceinline__ const T* grow(const void* base, int64_t sb, int64_t s
 template <typename T, int D>
 __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
-  typedef QImg<D> QI;
+  typedef QImg<T, D> QI;
   const goda_prefill_args& a = p.a;
   const int qt = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
   const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
@@ -195,7 +200,7 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
 template <typename T, int D>
 __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
-  typedef KVImg<D> KI;
+  typedef KVImg<T, D> KI;
   const goda_prefill_args& a = p.a;
   const int j = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
@@ -254,15 +259,17 @@ __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
 
 // Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
 // run LEAD MFMAs ahead (not all hoisted, which would hold 4 registers each).
-template <int NM, int LEAD>
+template <typename T, int NM, int LEAD>
 __device__ __forceinline__ void lead_schedule() {
-  __builtin_amdgcn_sched_group_barrier(0x100, LEAD, 0);
+  constexpr int M = kMfmaPerStep<T>;                            // MFMAs per step
+  constexpr int R = (int)sizeof(typename Vec<T>::v8) / 16;      // 16-byte reads per operand
+  __builtin_amdgcn_sched_group_barrier(0x100, LEAD * R, 0);
 #pragma unroll
   for (int i = 0; i < NM - LEAD; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, M, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, LEAD, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, LEAD * M, 0);
 }
 
 // Packs accumulator registers 8g..8g+7 of a 32x32 tile into an operand.
@@ -291,9 +298,9 @@ __device__ __forceinline__ V pack8(const float* x) {
 constexpr int kWavesKv = 8;
 constexpr int kKvStages = 3;
 
-template <int D>
+template <typename T, int D>
 struct DkvSmem {
-  static constexpr int64_t RING = kKvStages * QImg<D>::BYTES;
+  static constexpr int64_t RING = kKvStages * QImg<T, D>::BYTES;
   // operand exchange: [parity][pair][P0, P1, dS0, dS1][lane] 16-byte chunks
   static constexpr int64_t XBUF = 2 * 4 * 4 * 64 * 16;
   static constexpr int64_t BYTES = RING + XBUF;
@@ -303,14 +310,14 @@ template <typename T, int D, bool ALIBI>
 __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
-  typedef QImg<D> QI;
-  typedef KVImg<D> KI;
+  typedef QImg<T, D> QI;
+  typedef KVImg<T, D> KI;
   constexpr int KS = D / 16;  // k-steps over head_dim
   constexpr int MD = D / 32;  // 32-wide head_dim tiles of dK^T / dV^T
   constexpr int LOADS = 4 * QI::CH / (kWavesKv * 64);
   static_assert(4 * QI::CH % (kWavesKv * 64) == 0, "tile must split over the waves");
   extern __shared__ __align__(16) unsigned char smem[];
-  v8* xbuf = reinterpret_cast<v8*>(smem + DkvSmem<D>::RING);
+  v8* xbuf = reinterpret_cast<v8*>(smem + DkvSmem<T, D>::RING);
 
   const goda_prefill_args& a = p.a;
   const int b = blockIdx.z, hk = blockIdx.y;
@@ -347,13 +354,13 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
     const v8* src = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) stg[i] = src[tid + i * kWavesKv * 64];
-    if (tid < 16) stg_stat = src[QI::STAT + tid];
+    if (tid < QI::STAT_CH) stg_stat = src[QI::STAT + tid];
   };
   auto tile_store = [&](int it) {
     v8* dst = reinterpret_cast<v8*>(smem + (it % kKvStages) * QI::BYTES);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) dst[tid + i * kWavesKv * 64] = stg[i];
-    if (tid < 16) dst[QI::STAT + tid] = stg_stat;
+    if (tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
   };
   auto stage = [&](int it) { return reinterpret_cast<const v8*>(smem + (it % kKvStages) * QI::BYTES); };
   auto xchg = [&](int it, int c) -> v8& { return xbuf[(((it & 1) * 4 + pair) * 4 + c) * 64 + lane]; };
@@ -399,7 +406,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
           s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
           dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
         }
-        lead_schedule<2 * KS, 4>();
+        lead_schedule<T, 2 * KS, 4>();
         // P and dS; visibility as a range of the register's row offset
         // off = row - (q0 + 4 hi).
         const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
@@ -457,7 +464,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], p1, dv[md]);
         dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
       }
-      lead_schedule<4 * MD, 4>();
+      lead_schedule<T, 4 * MD, 4>();
     }
     if (it + 1 < n) tile_store(it + 1);
   }
@@ -516,8 +523,8 @@ template <typename T, int D, bool ALIBI>
 __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
-  typedef QImg<D> QI;
-  typedef KVImg<D> KI;
+  typedef QImg<T, D> QI;
+  typedef KVImg<T, D> KI;
   constexpr int KS = D / 16;
   constexpr int MD = D / 32;
   constexpr int NTH = kWavesWide * 64;
@@ -586,13 +593,13 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     const v8* src = src_of(it);
 #pragma unroll
     for (int i = 0; i < PART; ++i) stg[i] = src[tid + (part * PART + i) * NTH];
-    if (part == 0 && tid < 16) stg_stat = src[QI::STAT + tid];
+    if (part == 0 && tid < QI::STAT_CH) stg_stat = src[QI::STAT + tid];
   };
   auto store_part = [&](int it, int part) {
     v8* dst = reinterpret_cast<v8*>(smem + (it % 2) * QI::BYTES);
 #pragma unroll
     for (int i = 0; i < PART; ++i) dst[tid + (part * PART + i) * NTH] = stg[i];
-    if (part == 0 && tid < 16) dst[QI::STAT + tid] = stg_stat;
+    if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
   };
 
   const float c = p.scale_log2;
@@ -617,7 +624,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       v8* dst = reinterpret_cast<v8*>(smem + ((it + 1) % 2) * QI::BYTES);
 #pragma unroll
       for (int i = 0; i < PART; ++i) dst[tid + (part * PART + i) * NTH] = stg[i];
-      if (part == 0 && tid < 16) dst[QI::STAT + tid] = stg_stat;
+      if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
     };
 
     load_part(nx, 0);
@@ -628,7 +635,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
       dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
     }
-    lead_schedule<2 * KS, 4>();
+    lead_schedule<T, 2 * KS, 4>();
     store_next(0);
     load_part(nx, 1);
 
@@ -666,7 +673,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
       dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
     }
-    lead_schedule<2 * MD, 4>();
+    lead_schedule<T, 2 * MD, 4>();
     store_next(2);
     load_part(nx, 3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
@@ -675,7 +682,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
       dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
     }
-    lead_schedule<2 * MD, 4>();
+    lead_schedule<T, 2 * MD, 4>();
     store_next(3);
     ring_barrier();
   }
@@ -782,12 +789,12 @@ __global__ void __launch_bounds__(256) bwd_dkv_reduce_kernel(const BwdParams p) 
 // 4. dq
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool ALIBI>
-__global__ void __launch_bounds__(DqShape<D>::WAVES * 64, DqShape<D>::OCC) bwd_dq_mfma_kernel(const BwdParams p) {
-  constexpr int kWavesDq = DqShape<D>::WAVES;
+__global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::OCC)) bwd_dq_mfma_kernel(const BwdParams p) {
+  constexpr int kWavesDq = DqShape<T, D>::WAVES;
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
-  typedef QImg<D> QI;
-  typedef KVImg<D> KI;
+  typedef QImg<T, D> QI;
+  typedef KVImg<T, D> KI;
   constexpr int KS = D / 16;
   constexpr int MD = D / 32;
   constexpr int MT = kBKV / 32;   // 32-key blocks of S^T
@@ -888,7 +895,7 @@ __global__ void __launch_bounds__(DqShape<D>::WAVES * 64, DqShape<D>::OCC) bwd_d
         s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + l32], qf[ks], s[mt]);
         dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + l32], gf[ks], dp[mt]);
       }
-    lead_schedule<2 * KS * MT, 4>();
+    lead_schedule<T, 2 * KS * MT, 4>();
     // masks as ranges of the register's key offset off = key - (kvb + 4 hi)
     const int rel = kvb + 4 * hi;
     int hi_lim = g.lk - 1 - rel;
@@ -919,7 +926,7 @@ __global__ void __launch_bounds__(DqShape<D>::WAVES * 64, DqShape<D>::OCC) bwd_d
 #pragma unroll
       for (int md = 0; md < MD; ++md)
         dq[md] = mfma32(st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32], dsf[ks2], dq[md]);
-    lead_schedule<KS2 * MD, 4>();
+    lead_schedule<T, KS2 * MD, 4>();
   };
 
   if (n > 0) {
@@ -979,9 +986,9 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
   hipError_t e;
   if ((e = record_timing(p.g.timing_begin, s)) != hipSuccess) return e;
   if (a.seqlen_k > 0) {
-    if constexpr (D >= 256) {
+    if constexpr (DqShape<T, D>::WIDE) {
       auto kern = bwd_dkv_wide_kernel<T, D, ALIBI>;
-      const size_t lds = 2 * (size_t)QImg<D>::BYTES;
+      const size_t lds = 2 * (size_t)QImg<T, D>::BYTES;
       if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
         return e;
       const dim3 grid((a.seqlen_k + 32 * kWavesWide - 1) / (32 * kWavesWide), a.heads_kv * p.nsplit, a.batch);
@@ -994,7 +1001,7 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
       }
     } else {
       auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI>;
-      const size_t lds = (size_t)DkvSmem<D>::BYTES;
+      const size_t lds = (size_t)DkvSmem<T, D>::BYTES;
       if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
         return e;
       const dim3 grid((a.seqlen_k + 127) / 128, a.heads_kv, a.batch);
@@ -1004,10 +1011,10 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
   }
   if (a.seqlen_q > 0) {
     auto kern = bwd_dq_mfma_kernel<T, D, ALIBI>;
-    const size_t lds = 2 * (size_t)KVImg<D>::BYTES;
+    const size_t lds = 2 * (size_t)KVImg<T, D>::BYTES;
     if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
       return e;
-    constexpr int kWavesDq = DqShape<D>::WAVES;
+    constexpr int kWavesDq = DqShape<T, D>::WAVES;
     const int qb_rows = (kWavesDq / p.heads_per_wg) * 32;
     const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
     const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / p.heads_per_wg);
@@ -1023,7 +1030,7 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
 // causal key blocks differ in work by up to the sequence length), at most 8
 // and at most the (query head, query tile) pairs a key block can see.
 int dkv_splits(const goda_prefill_args& a) {
-  if (a.head_dim < 256 || a.heads_kv <= 0) return 1;
+  if ((a.head_dim < 256 && a.dtype != GODA_DTYPE_F32) || a.heads_kv <= 0) return 1;
   const int64_t wgs = (int64_t)((a.seqlen_k + 32 * kWavesWide - 1) / (32 * kWavesWide)) * a.heads_kv * a.batch;
   if (wgs <= 0) return 1;
   int64_t ns = (1024 + wgs - 1) / wgs;
@@ -1032,11 +1039,11 @@ int dkv_splits(const goda_prefill_args& a) {
   return (int)std::min<int64_t>(ns, 8);
 }
 
-template <int D>
+template <typename T, int D>
 int64_t workspace_bytes_d(const goda_prefill_args& a) {
   const int64_t ntq = (a.seqlen_q + kQRows - 1) / kQRows;
   const int64_t ntk = (a.seqlen_k + kBKV - 1) / kBKV;
-  int64_t bytes = (int64_t)a.batch * (ntq * a.heads_q * QImg<D>::BYTES + ntk * a.heads_kv * KVImg<D>::BYTES);
+  int64_t bytes = (int64_t)a.batch * (ntq * a.heads_q * QImg<T, D>::BYTES + ntk * a.heads_kv * KVImg<T, D>::BYTES);
   const int ns = dkv_splits(a);
   if (ns > 1) bytes += (int64_t)ns * 2 * a.batch * a.seqlen_k * a.heads_kv * D * 4;
   return bytes;
@@ -1047,11 +1054,11 @@ hipError_t launch_d(BwdParams p, hipStream_t s) {
   const goda_prefill_args& a = p.a;
   p.ntq = (a.seqlen_q + kQRows - 1) / kQRows;
   p.ntk = (a.seqlen_k + kBKV - 1) / kBKV;
-  p.heads_per_wg = gcd_int(p.group, DqShape<D>::WAVES);
+  p.heads_per_wg = gcd_int(p.group, DqShape<T, D>::WAVES);
   p.qimg = reinterpret_cast<unsigned char*>(p.g.workspace);
-  p.kvimg = p.qimg + (int64_t)a.batch * p.ntq * a.heads_q * QImg<D>::BYTES;
+  p.kvimg = p.qimg + (int64_t)a.batch * p.ntq * a.heads_q * QImg<T, D>::BYTES;
   p.nsplit = dkv_splits(a);
-  p.part = reinterpret_cast<float*>(p.kvimg + (int64_t)a.batch * p.ntk * a.heads_kv * KVImg<D>::BYTES);
+  p.part = reinterpret_cast<float*>(p.kvimg + (int64_t)a.batch * p.ntk * a.heads_kv * KVImg<T, D>::BYTES);
   hipError_t e;
   if (p.ntq > 0) {
     pack_q_bwd_kernel<T, D><<<dim3(p.ntq, a.heads_q, a.batch), 256, 0, s>>>(p);
@@ -1069,26 +1076,31 @@ template <typename T>
 hipError_t launch_t(const BwdParams& p, hipStream_t s) {
   if (p.a.head_dim == 64) return launch_d<T, 64>(p, s);
   if (p.a.head_dim == 128) return launch_d<T, 128>(p, s);
-  if (p.a.head_dim == 256) return launch_d<T, 256>(p, s);
+  if constexpr (sizeof(T) == 2) {
+    if (p.a.head_dim == 256) return launch_d<T, 256>(p, s);
+  }
   return hipErrorNotSupported;
 }
 
 }  // namespace
 
 bool prefill_bwd_mfma_supported(const goda_prefill_args& a) {
+  if (a.dtype == GODA_DTYPE_F32) return a.head_dim == 64 || a.head_dim == 128;
   if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16) return false;
   return a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256;
 }
 
 int64_t prefill_bwd_mfma_workspace_bytes(const goda_prefill_args& a) {
-  if (a.head_dim == 64) return workspace_bytes_d<64>(a);
-  if (a.head_dim == 128) return workspace_bytes_d<128>(a);
-  return workspace_bytes_d<256>(a);
+  if (a.dtype == GODA_DTYPE_F32) return a.head_dim == 64 ? workspace_bytes_d<float, 64>(a) : workspace_bytes_d<float, 128>(a);
+  if (a.head_dim == 64) return workspace_bytes_d<bf16, 64>(a);
+  if (a.head_dim == 128) return workspace_bytes_d<bf16, 128>(a);
+  return workspace_bytes_d<bf16, 256>(a);
 }
 
 hipError_t launch_prefill_bwd_mfma(BwdParams p, hipStream_t s) {
   if (p.a.dtype == GODA_DTYPE_BF16) return launch_t<bf16>(p, s);
   if (p.a.dtype == GODA_DTYPE_F16) return launch_t<f16>(p, s);
+  if (p.a.dtype == GODA_DTYPE_F32) return launch_t<float>(p, s);
   return hipErrorNotSupported;
 }
 
