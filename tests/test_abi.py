@@ -72,8 +72,12 @@ def test_workspace_size_positive_for_mfma_path(lib):
     need = lib.goda_attn_prefill_workspace_size(ctypes.byref(a))
     # K' and V^T tiles: 2 tensors x B x tiles x Hkv x 64 x D x 2 bytes
     assert need == 2 * 2 * 1 * 2 * 64 * 128 * 2
+    # fp32 at D=128 runs the same kernel with 32-key tiles of 4-byte elements
     a32 = _prefill_args(dtype=_lib.DTYPE_F32)
-    assert lib.goda_attn_prefill_workspace_size(ctypes.byref(a32)) == 0
+    assert lib.goda_attn_prefill_workspace_size(ctypes.byref(a32)) == 2 * 2 * 2 * 2 * 32 * 128 * 4
+    # fp32 at D=256 takes the generic kernel, which needs no workspace
+    a32w = _prefill_args(dtype=_lib.DTYPE_F32, head_dim=256)
+    assert lib.goda_attn_prefill_workspace_size(ctypes.byref(a32w)) == 0
 
 
 @pytest.mark.parametrize(
