@@ -20,9 +20,8 @@
 //           on 16x16x32 MFMA; K rows are loaded straight from the cache into
 //           the A operand (16 bytes per lane), Q^T lives in VGPRs. All query
 //           heads of the KV head's group are served by the same K/V bytes.
-//   values  O[head][d] += p[head][key] * V[key][d] on the vector ALUs: each
-//           lane owns 8 consecutive head-dim elements (16-byte loads, a wave
-//           instruction reads whole cache rows), p is broadcast through LDS.
+//   values  O[head][d] += p[head][key] * V[key][d] on the vector ALUs, p
+//           broadcast through LDS; the lane mapping is described at VRows.
 
 #include <map>
 #include <mutex>
@@ -69,6 +68,37 @@ struct V8<bf16> {
 template <>
 struct V8<f16> {
   typedef f16x8 t;
+};
+template <typename T>
+struct V4;
+template <>
+struct V4<bf16> {
+  typedef bf16x4 t;
+};
+template <>
+struct V4<f16> {
+  typedef f16x4 t;
+};
+
+// P.V lane mapping. Default: lane (kg, l16) owns head-dim chunks l16 (+16 i)
+// over the chunk's keys 4 kg .. 4 kg + 3, so the four key groups hold
+// partial sums of every output (reduced across lanes at the end). Slice
+// (head_dim 256): lane l owns head-dim elements D/64 * l .. + D/64 - 1 over
+// all 16 keys: a quarter of the accumulators (32 registers for 8 heads
+// instead of 128), no cross-lane reduction, and two waves per SIMD instead
+// of one.
+template <int D>
+constexpr bool kPvSlice = D >= 256;
+template <typename T, int D, bool SLICE>
+struct VRows;
+template <typename T, int D>
+struct VRows<T, D, false> {
+  typename V8<T>::t x[4][D / 128];  // keys 4 kg + kk, chunks l16 + 16 i
+};
+template <typename T, int D>
+struct VRows<T, D, true> {
+  static_assert(D / 64 == 4, "slice mapping: four elements per lane");
+  typename V4<T>::t x[kChunk];  // keys kk, elements 4 l .. 4 l + 3
 };
 
 // Wave-uniform copies (scalar registers) of values every lane holds equally.
@@ -206,6 +236,9 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   constexpr int KS = D / 32;    // k-steps of the 16x16x32 score MFMA
   constexpr int CPL = D / 128;  // 8-element head-dim chunks per lane in PV
   static_assert(CPL >= 1, "head_dim >= 128");
+  constexpr bool SLICE = kPvSlice<D>;
+  constexpr int NACC = SLICE ? D / 64 : CPL * 8;  // accumulators per head and lane
+  typedef VRows<T, D, SLICE> VR;
   const goda_decode_args& a = p.a;
 
   const int b = sg.b;
@@ -282,32 +315,39 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   const T* vbase = reinterpret_cast<const T*>(a.v_cache) + (int64_t)b * a.v_stride_b +
                    (int64_t)sg.hk * a.v_stride_h;
 
-  float acc[HMAX][CPL][8];
+  float acc[HMAX][NACC];
 #pragma unroll
   for (int h = 0; h < HMAX; ++h)
 #pragma unroll
-    for (int i = 0; i < CPL; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][i][e] = 0.f;
+    for (int i = 0; i < NACC; ++i) acc[h][i] = 0.f;
   float m_run = kNegInf, l_run = 0.f;  // for head l16 over this lane's keys
 
   // Each wave takes chunks wave, wave+4, ... of 16 keys.
   const int nchunks = (send - sbeg + kChunk - 1) / kChunk;
-  auto load = [&](int ch, v8 (&kf)[KS], v8 (&vf)[4][CPL]) {
+  auto load = [&](int ch, v8 (&kf)[KS], VR& vf) {
     const int k0 = sbeg + ch * kChunk;
     // K operand rows (clamped inside the segment; masked in the softmax).
     const T* kp = kbase + (int64_t)min(k0 + l16, send - 1) * a.k_stride_t;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = ld_vec<v8>(kp + 32 * ks + 8 * kg);
-    // V rows for the PV step: keys k0 + 4*kg + kk, head-dim chunk l16 (+16 i).
+    if constexpr (SLICE) {
+      // V rows for the PV step: every key of the chunk, elements 4 l .. 4 l + 3.
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const T* vp = vbase + (int64_t)min(k0 + 4 * kg + kk, send - 1) * a.v_stride_t;
+      for (int kk = 0; kk < kChunk; ++kk) {
+        const T* vp = vbase + (int64_t)min(k0 + kk, send - 1) * a.v_stride_t;
+        vf.x[kk] = ld_vec<typename V4<T>::t>(vp + 4 * lane);
+      }
+    } else {
+      // V rows for the PV step: keys k0 + 4*kg + kk, head-dim chunk l16 (+16 i).
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) vf[kk][i] = ld_vec<v8>(vp + 8 * (l16 + 16 * i));
+      for (int kk = 0; kk < 4; ++kk) {
+        const T* vp = vbase + (int64_t)min(k0 + 4 * kg + kk, send - 1) * a.v_stride_t;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) vf.x[kk][i] = ld_vec<v8>(vp + 8 * (l16 + 16 * i));
+      }
     }
   };
-  auto process = [&](int ch, const v8 (&kf)[KS], const v8 (&vf)[4][CPL]) {
+  auto process = [&](int ch, const v8 (&kf)[KS], const VR& vf) {
     const int k0 = sbeg + ch * kChunk;
     f32x4 sc = f32x4{};
 #pragma unroll
@@ -341,9 +381,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
 #pragma unroll
         for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-          for (int i = 0; i < CPL; ++i)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[4 * h4 + hh][i][e] *= al[hh];
+          for (int i = 0; i < NACC; ++i) acc[4 * h4 + hh][i] *= al[hh];
       }
     }
     const float m_use = (m_run == kNegInf) ? 0.f : m_run;
@@ -356,24 +394,43 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // Accumulate this lane's 4 keys for every head of the slice.
+    if constexpr (SLICE) {
+      // Every key of the chunk for this lane's elements and every head
+      // (p is read as a broadcast: all lanes load the same LDS words).
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      float vv[CPL][8];
+      for (int kk = 0; kk < kChunk; ++kk) {
+        float vv[NACC];
 #pragma unroll
-      for (int i = 0; i < CPL; ++i)
+        for (int e = 0; e < NACC; ++e) vv[e] = (float)vf.x[kk][e];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vv[i][e] = (float)vf[kk][i][e];
+        for (int h4 = 0; h4 < HMAX / 4; ++h4) {
+          const f32x4 pv = ld_vec<f32x4>(&sm.p[wave][kk][4 * h4]);
 #pragma unroll
-      for (int h4 = 0; h4 < HMAX / 4; ++h4) {
-        const f32x4 pv = ld_vec<f32x4>(&sm.p[wave][4 * kg + kk][4 * h4]);
+          for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-        for (int hh = 0; hh < 4; ++hh)
+            for (int e = 0; e < NACC; ++e) acc[4 * h4 + hh][e] = fmaf(pv[hh], vv[e], acc[4 * h4 + hh][e]);
+        }
+      }
+    } else {
+      // Accumulate this lane's 4 keys for every head of the slice.
 #pragma unroll
-          for (int i = 0; i < CPL; ++i)
+      for (int kk = 0; kk < 4; ++kk) {
+        float vv[CPL][8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-              acc[4 * h4 + hh][i][e] = fmaf(pv[hh], vv[i][e], acc[4 * h4 + hh][i][e]);
+        for (int i = 0; i < CPL; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vv[i][e] = (float)vf.x[kk][i][e];
+#pragma unroll
+        for (int h4 = 0; h4 < HMAX / 4; ++h4) {
+          const f32x4 pv = ld_vec<f32x4>(&sm.p[wave][4 * kg + kk][4 * h4]);
+#pragma unroll
+          for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i)
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                acc[4 * h4 + hh][8 * i + e] = fmaf(pv[hh], vv[i][e], acc[4 * h4 + hh][8 * i + e]);
+        }
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -384,7 +441,8 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   // Ring of NBUF register sets: chunk ch + (NBUF-1)*kWaves is in flight while
   // chunk ch is processed (the unrolled loop keeps every buffer index static).
   constexpr int NBUF = kNbuf<D>;
-  v8 kb[NBUF][KS], vb[NBUF][4][CPL];
+  v8 kb[NBUF][KS];
+  VR vb[NBUF];
 #pragma unroll
   for (int i = 0; i < NBUF - 1; ++i)
     if (wave + i * kWaves < nchunks) load(wave + i * kWaves, kb[i], vb[i]);
@@ -403,28 +461,32 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   // ---- reduce within the wave -------------------------------------------------
   l_run += shfl_xor_f(l_run, 16);
   l_run += shfl_xor_f(l_run, 32);
+  if (kg == 0 && l16 < HMAX) {
+    sm.m[wave][l16] = m_run;
+    sm.l[wave][l16] = l_run;
+  }
+  if constexpr (SLICE) {
 #pragma unroll
-  for (int h = 0; h < HMAX; ++h)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float v = acc[h][i][e];
-        v += shfl_xor_f(v, 16);
-        v += shfl_xor_f(v, 32);
-        acc[h][i][e] = v;
-      }
-  if (kg == 0) {
-    if (l16 < HMAX) {
-      sm.m[wave][l16] = m_run;
-      sm.l[wave][l16] = l_run;
-    }
+    for (int h = 0; h < HMAX; ++h)
+      st_vec<f32x4>(&sm.o[wave][h][4 * lane], f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]});
+  } else {
 #pragma unroll
     for (int h = 0; h < HMAX; ++h)
 #pragma unroll
-      for (int i = 0; i < CPL; ++i)
+      for (int i = 0; i < NACC; ++i) {
+        float v = acc[h][i];
+        v += shfl_xor_f(v, 16);
+        v += shfl_xor_f(v, 32);
+        acc[h][i] = v;
+      }
+    if (kg == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sm.o[wave][h][8 * (l16 + 16 * i) + e] = acc[h][i][e];
+      for (int h = 0; h < HMAX; ++h)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm.o[wave][h][8 * (l16 + 16 * i) + e] = acc[h][8 * i + e];
+    }
   }
   __syncthreads();
 
@@ -461,7 +523,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
 
 // Waves per SIMD the register allocation must allow (1: no constraint).
 template <int D, int HMAX>
-constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : 1;
+constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : kPvSlice<D> ? 2 : 1;
 
 // The kernel's only argument sits at offset 0 of the kernel argument segment
 // (reload_params reads it from there).
