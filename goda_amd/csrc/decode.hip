@@ -83,12 +83,15 @@ struct V4<f16> {
 // P.V lane mapping. Default: lane (kg, l16) owns head-dim chunks l16 (+16 i)
 // over the chunk's keys 4 kg .. 4 kg + 3, so the four key groups hold
 // partial sums of every output (reduced across lanes at the end). Slice
-// (head_dim 256): lane l owns head-dim elements D/64 * l .. + D/64 - 1 over
-// all 16 keys: a quarter of the accumulators (32 registers for 8 heads
-// instead of 128), no cross-lane reduction, and two waves per SIMD instead
-// of one.
-template <int D>
-constexpr bool kPvSlice = D >= 256;
+// (head_dim 256, or 16 query heads per workgroup): lane l owns head-dim
+// elements D/64 * l .. + D/64 - 1 over all 16 keys: a quarter of the
+// accumulators (D = 256, 8 heads: 32 registers instead of 128), no
+// cross-lane reduction, and two waves per SIMD instead of one (cfg5 decode
+// 94 -> 84 us; D = 128 with 16 heads 278 -> 212 us). With 4 or 8 heads at
+// D = 128 the default mapping already fits 3 or 2 waves per SIMD and its
+// 16-byte loads are 0-3% faster.
+template <int D, int HMAX>
+constexpr bool kPvSlice = D >= 256 || HMAX >= 16;
 template <typename T, int D, bool SLICE>
 struct VRows;
 template <typename T, int D>
@@ -97,8 +100,9 @@ struct VRows<T, D, false> {
 };
 template <typename T, int D>
 struct VRows<T, D, true> {
-  static_assert(D / 64 == 4, "slice mapping: four elements per lane");
-  typename V4<T>::t x[kChunk];  // keys kk, elements 4 l .. 4 l + 3
+  static constexpr int DPL = D / 64;
+  typedef T vec __attribute__((ext_vector_type(DPL)));
+  vec x[kChunk];  // keys kk, elements DPL l .. DPL l + DPL - 1
 };
 
 // Wave-uniform copies (scalar registers) of values every lane holds equally.
@@ -236,7 +240,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   constexpr int KS = D / 32;    // k-steps of the 16x16x32 score MFMA
   constexpr int CPL = D / 128;  // 8-element head-dim chunks per lane in PV
   static_assert(CPL >= 1, "head_dim >= 128");
-  constexpr bool SLICE = kPvSlice<D>;
+  constexpr bool SLICE = kPvSlice<D, HMAX>;
   constexpr int NACC = SLICE ? D / 64 : CPL * 8;  // accumulators per head and lane
   typedef VRows<T, D, SLICE> VR;
   const goda_decode_args& a = p.a;
@@ -331,11 +335,11 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = ld_vec<v8>(kp + 32 * ks + 8 * kg);
     if constexpr (SLICE) {
-      // V rows for the PV step: every key of the chunk, elements 4 l .. 4 l + 3.
+      // V rows for the PV step: every key of the chunk, this lane's elements.
 #pragma unroll
       for (int kk = 0; kk < kChunk; ++kk) {
         const T* vp = vbase + (int64_t)min(k0 + kk, send - 1) * a.v_stride_t;
-        vf.x[kk] = ld_vec<typename V4<T>::t>(vp + 4 * lane);
+        vf.x[kk] = ld_vec<typename VR::vec>(vp + NACC * lane);
       }
     } else {
       // V rows for the PV step: keys k0 + 4*kg + kk, head-dim chunk l16 (+16 i).
@@ -468,7 +472,8 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   if constexpr (SLICE) {
 #pragma unroll
     for (int h = 0; h < HMAX; ++h)
-      st_vec<f32x4>(&sm.o[wave][h][4 * lane], f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]});
+#pragma unroll
+      for (int e = 0; e < NACC; ++e) sm.o[wave][h][NACC * lane + e] = acc[h][e];
   } else {
 #pragma unroll
     for (int h = 0; h < HMAX; ++h)
@@ -523,7 +528,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
 
 // Waves per SIMD the register allocation must allow (1: no constraint).
 template <int D, int HMAX>
-constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : kPvSlice<D> ? 2 : 1;
+constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : kPvSlice<D, HMAX> ? 2 : 1;
 
 // The kernel's only argument sits at offset 0 of the kernel argument segment
 // (reload_params reads it from there).
