@@ -31,9 +31,9 @@
 // Q^T holds q * scale * log2(e) and the accumulators start at the row's
 // reference max m (negated) plus the ALiBi bias, so the scores leave the
 // MFMA as the exponents of P: the softmax spends no VALU instruction on
-// scaling, biasing or shifting them (the VALU work of a wave does not issue
-// while the other wave of its SIMD has matrix instructions waiting, so every
-// VALU instruction of the softmax lengthens the interval).
+// scaling, biasing or shifting them (every VALU instruction of the softmax
+// lengthens the interval: the two waves of a SIMD share its VALU, and the
+// row sums' packed dot products wait out the other wave's MFMAs).
 // Every query row lives in one lane pair (l, l^32), so the row max needs one
 // permlane32 swap and any rescale is lane-local.
 // Rescaling is lazy: a row's reference max only moves (and its O and l are
