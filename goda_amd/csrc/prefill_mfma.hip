@@ -18,9 +18,9 @@
 //      (query tile, query-head slice, sequence). All waves
 //      belong to query heads of ONE KV head, so every K/V tile streamed into
 //      LDS serves the whole query-head group ("read once per group"). Tiles
-//      move through a ring of 3 LDS stages: during the interval that reads
-//      tiles j and j+1, each wave loads its share of tile j+2 into registers
-//      and writes it to the free stage at the end. (Direct global->LDS DMA
+//      move through a ring of 4 LDS stages: during the interval that reads
+//      tiles j and j+1, each wave loads its share of tile j+3 into registers
+//      and writes it to a free stage (kStages below). (Direct global->LDS DMA
 //      would save those registers, but while such a load is in flight the
 //      compiler waits for ALL LDS reads before every MFMA operand use.)
 //
@@ -65,7 +65,16 @@ struct TileGeom {
   static constexpr int LOADS_PER_LANE = (K_CHUNKS + V_CHUNKS) / (64 * WAVES);  // 16-byte loads
   static_assert((K_CHUNKS + V_CHUNKS) % (64 * WAVES) == 0, "tile must split evenly over the waves");
 };
-constexpr int kStages = 3;  // LDS ring: tiles j, j+1 read, tile j+2 written
+// LDS ring of kStages tile stages: interval j reads tiles j (V) and j+1 (K)
+// and writes tile j + kAhead; a workgroup barrier opens every kBarrierEvery-th
+// interval. Safe when kAhead >= kBarrierEvery + 1 (every tile read was
+// written before the last barrier) and kStages >= kAhead + kBarrierEvery (no
+// stage is overwritten before every wave is past its last read).
+// (4 stages, tiles 3 intervals ahead, a barrier every interval: the extra
+// stage of prefetch is worth 1.5-2% at D = 256; halving the barriers with 5
+// stages changed nothing measurable.)
+constexpr int kStages = 4, kAhead = 3, kBarrierEvery = 1;
+static_assert(kAhead >= kBarrierEvery + 1 && kStages >= kAhead + kBarrierEvery, "ring shape");
 // Move each tile in two halves through half the staging registers: register
 // relief for D = 256 (whose two-waves-per-SIMD form is at the limit), and at
 // D = 128 half of the LDS stores move from the end of the interval, where
@@ -596,36 +605,33 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     __builtin_amdgcn_sched_group_barrier(0x008, kLead * (kMfma / kReads), 0);
   };
 
-  // Start of the ring interval that reads tiles j (V) and j+1 (K). Past the
-  // barrier, tile j+1 (written at the end of the previous interval) is
-  // visible and nobody reads the stage of tile j-1, which tile j+2 takes over
-  // at the end of this interval; its global loads are issued now.
+  // Start of the ring interval that reads tiles j (V) and j+1 (K) and writes
+  // tile j + kAhead (its global loads are issued now, its LDS stores go out
+  // mid-interval and at the end).
   auto ring_begin = [&](int j) {
-    ring_barrier();
-    if (j + 2 < j_hi) tile_load_part(j + 2, 0);
+    if ((j - j_lo) % kBarrierEvery == kBarrierEvery - 1) ring_barrier();  // the prologue's barrier opens interval j_lo
+    if (j + kAhead < j_hi) tile_load_part(j + kAhead, 0);
   };
   auto ring_mid = [&](int j) {
     if constexpr (SPLIT) {
-      if (j + 2 < j_hi) {
-        tile_store_part(j + 2, 0);
-        tile_load_part(j + 2, 1);
+      if (j + kAhead < j_hi) {
+        tile_store_part(j + kAhead, 0);
+        tile_load_part(j + kAhead, 1);
       }
     }
   };
   auto ring_end = [&](int j) {
-    if (j + 2 < j_hi) tile_store(j + 2);
+    if (j + kAhead < j_hi) tile_store(j + kAhead);
   };
 
-  // ---- prologue: tiles j_lo and j_lo+1 resident, scores of tile j_lo ------------------
+  // ---- prologue: tiles j_lo .. j_lo + kAhead - 1 resident, scores of tile j_lo --------
   const int ntile = j_hi - j_lo;
   f32x16 s_a[MT][NT];
   v8 pf[NT][KS2];
   if (ntile > 0) {
-    tile_load(j_lo);
-    tile_store(j_lo);
-    if (ntile > 1) {
-      tile_load(j_lo + 1);
-      tile_store(j_lo + 1);
+    for (int t = 0; t < kAhead && t < ntile; ++t) {
+      tile_load(j_lo + t);
+      tile_store(j_lo + t);
     }
     ring_barrier();
     qk(j_lo, s_a);
