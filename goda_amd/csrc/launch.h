@@ -18,6 +18,7 @@ struct PrefillParams {
   int kv_tile;        // keys per workspace tile (MFMA path)
   int ntiles_k;       // ceil(seqlen_k / kv_tile)
   int heads_per_wg;   // query heads sharing one workgroup (MFMA path)
+  int qtiles;         // query tiles per (sequence, head slice) in the grid (MFMA path)
 };
 
 struct DecodeParams {

@@ -75,6 +75,12 @@ struct TileGeom {
 // stages changed nothing measurable.)
 constexpr int kStages = 4, kAhead = 3, kBarrierEvery = 1;
 static_assert(kAhead >= kBarrierEvery + 1 && kStages >= kAhead + kBarrierEvery, "ring shape");
+// Packed batches: the query tiles of each (sequence, head slice) pair are dealt
+// round-robin over a group of this many XCDs (see the workgroup order below).
+// Kernel time over five packed batches (cfg5's and three other draws of 16
+// lengths in [128, 4096], one of 16 in [512, 8192]): 8 XCDs 3379 us, groups
+// of 4 3391, of 2 3752, whole pairs per XCD 4024.
+constexpr int kVarlenXcdGroup = 8;
 // Move each tile in two halves through half the staging registers: register
 // relief for D = 256 (whose two-waves-per-SIMD form is at the limit), and at
 // D = 128 half of the LDS stores move from the end of the interval, where
@@ -291,17 +297,34 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   const int hg = p.heads_per_wg;
   const int nslices = p.group / hg;
   const int qb_rows = (WAVES / hg) * 32 * NT;  // query rows per workgroup
-  const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
+  const int nqt = p.qtiles;
 
-  // XCD-aware order: consecutive dispatch slots rotate over the 8 XCDs; each
-  // XCD gets a contiguous range of (sequence, head-slice) pairs so the
-  // workgroups sharing K/V tiles share that XCD's L2. Heavy causal query
-  // tiles go first.
+  // XCD-aware order: consecutive dispatch slots rotate over the 8 XCDs
+  // (XCD = blockIdx % 8). Dense batches: each XCD gets a contiguous range of
+  // (sequence, head-slice) pairs, so the workgroups sharing K/V tiles share
+  // that XCD's L2; heavy causal query tiles go first. Packed batches of
+  // unequal lengths would leave the XCDs very unequally loaded that way
+  // (random draws of 16 lengths in [128, 4096]: busiest XCD 1.5-2x the mean),
+  // so there XCD x takes the query tiles qt = x (mod kXg) of the pairs of its
+  // group, pair after pair, heaviest tile first: every XCD stays within ~3%
+  // of the mean, and the XCDs work on the same pair at the same time, so each
+  // XCD's L2 still serves one pair's K/V stream to all its workgroups.
   const int nblk = gridDim.x;
   const int lin = blockIdx.x;
-  const int vid = (nblk % 8 == 0) ? (lin % 8) * (nblk / 8) + lin / 8 : lin;
-  const int pair = vid / nqt;
-  const int qt = nqt - 1 - (vid % nqt);
+  int pair, qt;
+  constexpr int kXg = kVarlenXcdGroup;  // XCDs sharing one pair's query tiles
+  const int npairs = nblk / nqt;
+  if (a.cu_seqlens_q && nblk % 8 == 0 && nqt % kXg == 0 && npairs % (8 / kXg) == 0) {
+    const int x = lin % 8, s = lin / 8;
+    const int per = nqt / kXg;                 // query tiles of one pair on one XCD
+    const int pg = npairs / (8 / kXg);         // pairs of one XCD group
+    pair = (x / kXg) * pg + s / per;
+    qt = (per - 1 - s % per) * kXg + x % kXg;
+  } else {
+    const int vid = (nblk % 8 == 0) ? (lin % 8) * (nblk / 8) + lin / 8 : lin;
+    pair = vid / nqt;
+    qt = nqt - 1 - (vid % nqt);
+  }
   const int b = pair / (a.heads_kv * nslices);
   const int rem = pair % (a.heads_kv * nslices);
   const int hk = rem / nslices;
@@ -737,7 +760,9 @@ hipError_t launch_attn(PrefillParams p, hipStream_t s) {
   const int hg = gcd_int(p.group, C::WAVES);
   p.heads_per_wg = hg;
   const int qb_rows = (C::WAVES / hg) * 32 * C::NT;
-  const int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
+  int nqt = (a.seqlen_q + qb_rows - 1) / qb_rows;
+  if (a.cu_seqlens_q) nqt = (nqt + 7) / 8 * 8;  // whole rounds over the 8 XCDs (extra tiles exit at once)
+  p.qtiles = nqt;
   const int64_t nblk = (int64_t)nqt * a.batch * a.heads_kv * (p.group / hg);
   if (nblk <= 0) return hipSuccess;
   if (nblk > 0x7fffffff) return hipErrorInvalidValue;
