@@ -320,6 +320,22 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     const int pg = npairs / (8 / kXg);         // pairs of one XCD group
     pair = (x / kXg) * pg + s / per;
     qt = (per - 1 - s % per) * kXg + x % kXg;
+    if (a.batch <= 64) {
+      // Longest sequences first, so the heaviest tiles are not the last ones
+      // dispatched: position `pair` in the walk is served by the sequence of
+      // that length rank (ties by index; one wave-wide pass over the lengths).
+      const int per_seq = npairs / a.batch;  // pairs of one sequence
+      const int r = pair / per_seq;
+      const int ln = threadIdx.x & 63;
+      const int len = ln < a.batch ? a.cu_seqlens_q[ln + 1] - a.cu_seqlens_q[ln] : -1;
+      int rank = 0;
+      for (int j = 0; j < a.batch; ++j) {
+        const int lj = __shfl(len, j, 64);
+        rank += (lj > len || (lj == len && j < ln)) ? 1 : 0;
+      }
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(ln < a.batch && rank == r);
+      pair = __builtin_ctzll(hit) * per_seq + pair % per_seq;
+    }
   } else {
     const int vid = (nblk % 8 == 0) ? (lin % 8) * (nblk / 8) + lin / 8 : lin;
     pair = vid / nqt;
