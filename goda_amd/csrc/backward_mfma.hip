@@ -175,7 +175,14 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
     float dl = 0.f;
     if (i < g.lq) {
       const T* orow = grow<T>(a.o, a.o_stride_b, a.o_stride_t, a.o_stride_h, varlen, b, g.q_row0 + i, hq);
-      for (int d = part; d < D; d += 8) dl = fmaf((float)orow[d], (float)grows[r][d], dl);
+      // 16-byte loads: the row's 8 threads read 8 consecutive chunks at a time
+#pragma unroll
+      for (int c = 8 * part; c < D; c += 64) {
+        const v8 ov = ld_vec<v8>(orow + c);
+        const v8 gv = ld_vec<v8>(&grows[r][c]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dl = fmaf((float)ov[e], (float)gv[e], dl);
+      }
     }
     dl += shfl_xor_f(dl, 1);
     dl += shfl_xor_f(dl, 2);
