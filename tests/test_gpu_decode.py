@@ -176,7 +176,7 @@ def test_kv_append_then_decode(dtype):
 
 
 # ---------------------------------------------------------------------------
-# BASELINE decode workloads at full size
+# the benchmark decode workloads (cfg4, cfg5) at full size
 # ---------------------------------------------------------------------------
 def _check_decode_workload(w: wl.Decode, seqs: list[int]):
     inp = wl.decode_inputs(w, DEV)

@@ -189,7 +189,7 @@ def test_prefill_rejects_bad_args():
 
 
 # ---------------------------------------------------------------------------
-# the BASELINE workloads
+# the benchmark prefill workloads (cfg1-cfg5)
 # ---------------------------------------------------------------------------
 def _sample_rows(t: int, n: int, seed: int) -> torch.Tensor:
     g = torch.Generator().manual_seed(seed)
