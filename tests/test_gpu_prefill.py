@@ -149,6 +149,33 @@ def test_prefill_varlen(dtype, d, hq, hkv):
     assert max_err(o, o_ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("nseq", [40, 70])
+def test_prefill_varlen_many_sequences(nseq):
+    """Packed batches walk their (sequence, head) pairs longest sequence first
+    when there are at most 64 sequences (ranked on the device, ties by index)
+    and in index order above that; both must cover every query tile once.
+    Lengths include repeats (rank ties), an empty sequence and a long one."""
+    g = torch.Generator().manual_seed(nseq)
+    lens = torch.randint(1, 160, (nseq,), generator=g)
+    lens[3] = lens[7] = lens[11]  # ties
+    lens[5] = 0
+    lens[nseq - 2] = 700
+    lens = lens.tolist()
+    hq, hkv, d = 4, 2, 128
+    cu = torch.zeros(nseq + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    total = int(cu[-1])
+    q = _rand((total, hq, d), torch.bfloat16, 31)
+    k = _rand((total, hkv, d), torch.bfloat16, 32)
+    v = _rand((total, hkv, d), torch.bfloat16, 33)
+    o = ops.attention_prefill(
+        q.to(DEV), k.to(DEV), v.to(DEV), causal=True,
+        cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(lens), max_seqlen_k=max(lens),
+    )
+    o_ref = ref.varlen_attention(q, k, v, cu, cu, causal=True)
+    assert max_err(o, o_ref) <= TOL[torch.bfloat16]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_prefill_seqused_k(dtype):
     """Per-sequence key counts from the device (chunked prefill over a cache)."""
