@@ -108,6 +108,16 @@ def test_backward_d256_paths(dtype):
     _case(1, 50, 170, 8, 2, 256, dtype, causal=True, rope=True, seed=14)
 
 
+def test_backward_workgroup_order_partial_chunks():
+    """The dk/dv and dq grids are walked in chunks of 16 (head group or pair)
+    units, heaviest block of each unit first; unit counts that leave a partial
+    last chunk (3 x 6 = 18 units at head_dim 128; 5 x 2 x splits at 256 with
+    the split dk/dv walk) must still visit every block exactly once."""
+    _case(3, 160, 160, 12, 6, 128, torch.bfloat16, causal=True, seed=21)
+    _case(5, 130, 130, 8, 2, 256, torch.bfloat16, causal=True, rope=True, seed=22)
+    _case(3, 70, 70, 12, 6, 128, torch.float32, causal=True, seed=23)
+
+
 def test_backward_rows_without_keys():
     """Lq > Lk with causal: the first Lq - Lk rows see no key; their o is 0
     and they contribute nothing (checked against the float64 brute force,
