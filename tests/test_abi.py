@@ -5,8 +5,10 @@ validation rejects bad arguments (no GPU work is launched here)."""
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -130,3 +132,20 @@ def test_ops_refuse_cpu_tensors():
         ops.attention_prefill(q, q, q, causal=True)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.attention_decode(q[:, 0], q, q, torch.zeros(1, dtype=torch.int32))
+
+
+def test_missing_library_is_a_loud_error(tmp_path):
+    """With no built library the package refuses to run (there is no CPU or
+    SDPA fallback): loading raises and names the build command."""
+    code = (
+        "import goda_amd._lib as L\n"
+        "try:\n"
+        "    L.load()\n"
+        "except RuntimeError as e:\n"
+        "    print('raised:', e)\n"
+        "else:\n"
+        "    print('loaded')\n"
+    )
+    env = dict(os.environ, GODA_ATTN_LIB=str(tmp_path / "nope" / "libgoda_attn.so"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300, cwd=str(ROOT))
+    assert "raised:" in out.stdout and "no non-HIP fallback" in out.stdout, out.stdout + out.stderr
