@@ -34,7 +34,8 @@
  *     as applied to q and k before RoPE (mint/nn/attn.py:57-60): a head row
  *     x becomes x * rsqrt(mean(x^2) + norm_eps) * (1 + w) in fp32, with a
  *     caller supplied fp32 weight w [head_dim] (the module's `scale`);
- *   - lse = ln(sum_j exp(score_ij)) over the scaled, biased, unmasked scores
+ *   - lse = ln(sum_j exp(score_ij)) over the scaled, biased scores of the
+ *     visible keys
  *     (kernels_/flash_attn_gqa/cuda.py:496-499). A row with no visible key
  *     produces o = 0 and lse = -inf.
  *
