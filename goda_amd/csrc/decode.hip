@@ -1,4 +1,4 @@
-// One-token decode attention over a contiguous KV cache (bf16 / fp16) with
+// One-token decode attention over a contiguous KV cache (bf16 / fp16 / fp32) with
 // per-sequence lengths, plus the KV append.
 //
 // Work decomposition (balanced split-K). The visible keys of every unit
@@ -69,6 +69,10 @@ template <>
 struct V8<f16> {
   typedef f16x8 t;
 };
+template <>
+struct V8<float> {
+  typedef f32x8 t;
+};
 template <typename T>
 struct V4;
 template <>
@@ -78,6 +82,10 @@ struct V4<bf16> {
 template <>
 struct V4<f16> {
   typedef f16x4 t;
+};
+template <>
+struct V4<float> {
+  typedef f32x4 t;
 };
 
 // P.V lane mapping. Default: lane (kg, l16) owns head-dim chunks l16 (+16 i)
@@ -526,14 +534,16 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   __syncthreads();
 }
 
-// Waves per SIMD the register allocation must allow (1: no constraint).
-template <int D, int HMAX>
-constexpr int kDecodeOcc = (D == 128 && HMAX == 4) ? 3 : kPvSlice<D, HMAX> ? 2 : 1;
+// Waves per SIMD the register allocation must allow (1: no constraint). fp32
+// operands and V rows take twice the registers of 16-bit ones.
+template <typename T, int D, int HMAX>
+constexpr int kDecodeOcc = sizeof(T) == 4 ? ((D == 128 && HMAX == 4) ? 2 : 1)
+                                          : (D == 128 && HMAX == 4) ? 3 : kPvSlice<D, HMAX> ? 2 : 1;
 
 // The kernel's only argument sits at offset 0 of the kernel argument segment
 // (reload_params reads it from there).
 template <typename T, int D, int HMAX>
-__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<D, HMAX>)))
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(kDecodeOcc<T, D, HMAX>)))
 decode_splitk_kernel(const DecodeParams p) {
   __shared__ DecodeSmem<D, HMAX> sm;
   const goda_decode_args& a = p.a;
@@ -790,7 +800,7 @@ hipError_t launch_append_t(const goda_kv_append_args& a, hipStream_t s) {
 }  // namespace
 
 bool decode_mfma_supported(const goda_decode_args& a) {
-  if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16) return false;
+  if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16 && a.dtype != GODA_DTYPE_F32) return false;
   return a.head_dim == 128 || a.head_dim == 256;
 }
 
@@ -815,6 +825,7 @@ int64_t decode_workspace_bytes(const goda_decode_args& a) {
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s) {
   if (p.a.dtype == GODA_DTYPE_BF16) return launch_t<bf16>(p, s);
   if (p.a.dtype == GODA_DTYPE_F16) return launch_t<f16>(p, s);
+  if (p.a.dtype == GODA_DTYPE_F32) return launch_t<float>(p, s);
   return hipErrorNotSupported;
 }
 
