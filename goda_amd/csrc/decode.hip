@@ -91,7 +91,7 @@ struct V4<float> {
 // P.V lane mapping. Default: lane (kg, l16) owns head-dim chunks l16 (+16 i)
 // over the chunk's keys 4 kg .. 4 kg + 3, so the four key groups hold
 // partial sums of every output (reduced across lanes at the end). Slice
-// (head_dim 256, or 16 query heads per workgroup): lane l owns head-dim
+// (head_dim 64 or 256, or 16 query heads per workgroup): lane l owns head-dim
 // elements D/64 * l .. + D/64 - 1 over all 16 keys: a quarter of the
 // accumulators (D = 256, 8 heads: 32 registers instead of 128), no
 // cross-lane reduction, and two waves per SIMD instead of one (cfg5 decode
@@ -99,7 +99,7 @@ struct V4<float> {
 // D = 128 the default mapping already fits 3 or 2 waves per SIMD and its
 // 16-byte loads are 0-3% faster.
 template <int D, int HMAX>
-constexpr bool kPvSlice = D >= 256 || HMAX >= 16;
+constexpr bool kPvSlice = D != 128 || HMAX >= 16;  // head_dim 64 and 256, or 16 heads
 template <typename T, int D, bool SLICE>
 struct VRows;
 template <typename T, int D>
@@ -247,8 +247,8 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
   typedef typename V8<T>::t v8;
   constexpr int KS = D / 32;    // k-steps of the 16x16x32 score MFMA
   constexpr int CPL = D / 128;  // 8-element head-dim chunks per lane in PV
-  static_assert(CPL >= 1, "head_dim >= 128");
   constexpr bool SLICE = kPvSlice<D, HMAX>;
+  static_assert(CPL >= 1 || SLICE, "the default mapping needs head_dim >= 128");
   constexpr int NACC = SLICE ? D / 64 : CPL * 8;  // accumulators per head and lane
   typedef VRows<T, D, SLICE> VR;
   const goda_decode_args& a = p.a;
@@ -700,6 +700,7 @@ hipError_t launch_d(const DecodeParams& p, hipStream_t s) {
 
 template <typename T>
 hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
+  if (p.a.head_dim == 64) return launch_d<T, 64>(p, s);
   if (p.a.head_dim == 128) return launch_d<T, 128>(p, s);
   if (p.a.head_dim == 256) return launch_d<T, 256>(p, s);
   return hipErrorNotSupported;
@@ -801,7 +802,7 @@ hipError_t launch_append_t(const goda_kv_append_args& a, hipStream_t s) {
 
 bool decode_mfma_supported(const goda_decode_args& a) {
   if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16 && a.dtype != GODA_DTYPE_F32) return false;
-  return a.head_dim == 128 || a.head_dim == 256;
+  return a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256;
 }
 
 int64_t decode_slots(const goda_decode_args& a) {

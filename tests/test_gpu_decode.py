@@ -58,7 +58,7 @@ def _decode_case(b, hq, hkv, d, lmax, lens, dtype, *, split=0, window=-1, alibi=
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 1), (4, 4), (16, 1), (6, 2)])
 def test_decode_shapes(dtype, d, hq, hkv):
     lens = [1, 7, 64, 65, 300, 513, 1000]
