@@ -29,6 +29,9 @@ ERR_UNSUPPORTED = -2
 ERR_WORKSPACE = -3
 ERR_HIP = -4
 
+# Size of the device-resident scratch array of goda_attn_decode_noalloc.
+DECODE_NOALLOC_SCRATCH_BYTES = 36 << 20
+
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
@@ -205,6 +208,7 @@ SYMBOLS = {
     "goda_attn_prefill_bwd": (_i32, [ctypes.POINTER(PrefillArgs), ctypes.POINTER(PrefillGrads), _vp]),
     "goda_attn_decode_workspace_size": (_i64, [ctypes.POINTER(DecodeArgs)]),
     "goda_attn_decode": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
+    "goda_attn_decode_noalloc": (_i32, [ctypes.POINTER(DecodeArgs), _vp]),
     "goda_attn_kv_append": (_i32, [ctypes.POINTER(KvAppendArgs), _vp]),
 }
 

@@ -93,6 +93,50 @@ goda::PrefillParams make_prefill_params(const goda_prefill_args* a) {
   return p;
 }
 
+// Checks of goda_attn_decode / goda_attn_decode_noalloc (everything but the
+// workspace); returns GODA_OK or a failure status.
+int32_t check_decode(const goda_decode_args* a) {
+  if (!a) return fail(GODA_ERR_INVALID_ARG, "decode: args is NULL");
+  if (!dtype_ok(a->dtype)) return fail(GODA_ERR_INVALID_ARG, "decode: unknown dtype %d", a->dtype);
+  if (a->batch < 0 || a->max_seqlen < 0)
+    return fail(GODA_ERR_INVALID_ARG, "decode: negative size (batch %d, max_seqlen %d)", a->batch,
+                a->max_seqlen);
+  if (a->heads_q <= 0 || a->heads_kv <= 0 || a->heads_q % a->heads_kv != 0)
+    return fail(GODA_ERR_INVALID_ARG, "decode: heads_q %d must be a positive multiple of heads_kv %d",
+                a->heads_q, a->heads_kv);
+  if (!head_dim_ok(a->head_dim))
+    return fail(GODA_ERR_UNSUPPORTED, "decode: head_dim %d not in {64, 128, 256}", a->head_dim);
+  if (a->split_size < 0 || (a->split_size > 0 && a->split_size % 64 != 0))
+    return fail(GODA_ERR_INVALID_ARG, "decode: split_size %d must be 0 or a positive multiple of 64",
+                a->split_size);
+  if (!(a->softmax_scale > 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "decode: softmax_scale must be positive (got %g)", (double)a->softmax_scale);
+  if (a->q_norm_weight && !(a->norm_eps >= 0.f))
+    return fail(GODA_ERR_INVALID_ARG, "decode: norm_eps must be >= 0 (got %g)", (double)a->norm_eps);
+  if (a->batch == 0) return GODA_OK;
+  if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->cache_seqlens)
+    return fail(GODA_ERR_INVALID_ARG, "decode: NULL tensor pointer");
+  if (a->rope_q) {
+    if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
+      return fail(GODA_ERR_INVALID_ARG, "decode: RoPE requested without cos/sin tables");
+    if (a->rope_q_offset < 0 || (int64_t)a->rope_q_offset + a->max_seqlen - 1 >= a->rope_len)
+      return fail(GODA_ERR_INVALID_ARG, "decode: q positions up to %lld exceed rope_len %d",
+                  (long long)a->rope_q_offset + a->max_seqlen - 1, a->rope_len);
+  }
+  return GODA_OK;
+}
+
+goda::DecodeParams make_decode_params(const goda_decode_args& a) {
+  goda::DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.a = a;
+  p.group = a.heads_q / a.heads_kv;
+  p.scale_log2 = a.softmax_scale * 1.4426950408889634f;
+  p.split = a.split_size;
+  p.nslots = goda::decode_slots(a);
+  return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -161,103 +205,43 @@ int32_t goda_attn_prefill_bwd(const goda_prefill_args* a, const goda_prefill_gra
 
 int64_t goda_attn_decode_workspace_size(const goda_decode_args* a) {
   if (!a) return fail(GODA_ERR_INVALID_ARG, "decode: args is NULL");
-  if (!goda::decode_mfma_supported(*a)) return 0;
-  if (a->heads_q <= 0 || a->heads_kv <= 0 || a->heads_q % a->heads_kv != 0)
-    return fail(GODA_ERR_INVALID_ARG, "decode: heads_q %d must be a positive multiple of heads_kv %d",
-                a->heads_q, a->heads_kv);
-  return goda::decode_workspace_bytes(*a);
-}
-
-int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
-  if (!a) return fail(GODA_ERR_INVALID_ARG, "decode: args is NULL");
-  if (!dtype_ok(a->dtype)) return fail(GODA_ERR_INVALID_ARG, "decode: unknown dtype %d", a->dtype);
-  if (a->batch < 0 || a->max_seqlen < 0)
-    return fail(GODA_ERR_INVALID_ARG, "decode: negative size (batch %d, max_seqlen %d)", a->batch,
-                a->max_seqlen);
   if (a->heads_q <= 0 || a->heads_kv <= 0 || a->heads_q % a->heads_kv != 0)
     return fail(GODA_ERR_INVALID_ARG, "decode: heads_q %d must be a positive multiple of heads_kv %d",
                 a->heads_q, a->heads_kv);
   if (!head_dim_ok(a->head_dim))
     return fail(GODA_ERR_UNSUPPORTED, "decode: head_dim %d not in {64, 128, 256}", a->head_dim);
-  if (a->split_size < 0 || (a->split_size > 0 && a->split_size % 64 != 0))
-    return fail(GODA_ERR_INVALID_ARG, "decode: split_size %d must be 0 or a positive multiple of 64",
-                a->split_size);
-  if (!(a->softmax_scale > 0.f))
-    return fail(GODA_ERR_INVALID_ARG, "decode: softmax_scale must be positive (got %g)", (double)a->softmax_scale);
-  if (a->q_norm_weight && !(a->norm_eps >= 0.f))
-    return fail(GODA_ERR_INVALID_ARG, "decode: norm_eps must be >= 0 (got %g)", (double)a->norm_eps);
+  return goda::decode_workspace_bytes(*a);
+}
+
+int32_t goda_attn_decode(const goda_decode_args* a, void* stream) {
+  const int32_t st = check_decode(a);
+  if (st != GODA_OK) return st;
   if (a->batch == 0) return ok();
-  if (!a->q || !a->k_cache || !a->v_cache || !a->o || !a->cache_seqlens)
-    return fail(GODA_ERR_INVALID_ARG, "decode: NULL tensor pointer");
-  if (a->rope_q) {
-    if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
-      return fail(GODA_ERR_INVALID_ARG, "decode: RoPE requested without cos/sin tables");
-    if (a->rope_q_offset < 0 || (int64_t)a->rope_q_offset + a->max_seqlen - 1 >= a->rope_len)
-      return fail(GODA_ERR_INVALID_ARG, "decode: q positions up to %lld exceed rope_len %d",
-                  (long long)a->rope_q_offset + a->max_seqlen - 1, a->rope_len);
-  }
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (goda::decode_mfma_supported(*a)) {
-    goda::DecodeParams p;
-    memset(&p, 0, sizeof(p));
-    p.a = *a;
-    p.group = a->heads_q / a->heads_kv;
-    p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
-    p.split = a->split_size;
-    p.nslots = goda::decode_slots(*a);
-    const int64_t need = goda::decode_workspace_bytes(*a);
-    if (need > 0 && (!a->workspace || a->workspace_bytes < need))
-      return fail(GODA_ERR_WORKSPACE, "decode: workspace of %lld bytes needed, %lld given",
-                  (long long)need, (long long)a->workspace_bytes);
-    return hip_status(goda::launch_decode(p, s), "decode");
-  }
-  // Other dtypes / head dims: the generic prefill kernel with one query row
-  // per sequence and seqused_k = cache_seqlens (bottom-right alignment puts
-  // the query at position cache_seqlens[b] - 1).
-  goda_prefill_args pa;
-  memset(&pa, 0, sizeof(pa));
-  pa.dtype = a->dtype;
-  pa.batch = a->batch;
-  pa.heads_q = a->heads_q;
-  pa.heads_kv = a->heads_kv;
-  pa.head_dim = a->head_dim;
-  pa.seqlen_q = 1;
-  pa.seqlen_k = a->max_seqlen;
-  pa.causal = 1;
-  pa.window_left = a->window_left;
-  pa.softmax_scale = a->softmax_scale;
-  pa.q = a->q;
-  pa.q_stride_b = a->q_stride_b;
-  pa.q_stride_t = 0;
-  pa.q_stride_h = a->q_stride_h;
-  pa.k = a->k_cache;
-  pa.k_stride_b = a->k_stride_b;
-  pa.k_stride_t = a->k_stride_t;
-  pa.k_stride_h = a->k_stride_h;
-  pa.v = a->v_cache;
-  pa.v_stride_b = a->v_stride_b;
-  pa.v_stride_t = a->v_stride_t;
-  pa.v_stride_h = a->v_stride_h;
-  pa.o = a->o;
-  pa.o_stride_b = a->o_stride_b;
-  pa.o_stride_t = 0;
-  pa.o_stride_h = a->o_stride_h;
-  pa.lse = a->lse;
-  pa.lse_stride_b = a->lse_stride_b;
-  pa.lse_stride_h = 1;
-  pa.seqused_k = a->cache_seqlens;
-  pa.alibi_slopes = a->alibi_slopes;
-  pa.rope_cos = a->rope_cos;
-  pa.rope_sin = a->rope_sin;
-  pa.rope_len = a->rope_len;
-  pa.rope_q = a->rope_q;
-  pa.rope_q_offset = a->rope_q_offset;
-  pa.q_norm_weight = a->q_norm_weight;
-  pa.norm_eps = a->norm_eps;
-  pa.timing_begin = a->timing_begin;
-  pa.timing_end = a->timing_end;
-  goda::PrefillParams p = make_prefill_params(&pa);
-  return hip_status(goda::launch_prefill_generic(p, s), "decode");
+  const int64_t need = goda::decode_workspace_bytes(*a);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need))
+    return fail(GODA_ERR_WORKSPACE, "decode: workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)a->workspace_bytes);
+  return hip_status(goda::launch_decode(make_decode_params(*a), reinterpret_cast<hipStream_t>(stream)), "decode");
+}
+
+int32_t goda_attn_decode_noalloc(const goda_decode_args* a, void* stream) {
+  const int32_t st = check_decode(a);
+  if (st != GODA_OK) return st;
+  if (a->batch == 0) return ok();
+  const int64_t need = goda::decode_workspace_bytes(*a);
+  if (need > goda::kDecodeScratchBytes)
+    return fail(GODA_ERR_WORKSPACE,
+                "decode_noalloc: the split-K partials need %lld bytes, more than the %lld-byte scratch array "
+                "(use split_size 0 or a larger split, or goda_attn_decode with a workspace)",
+                (long long)need, (long long)goda::kDecodeScratchBytes);
+  goda_decode_args b = *a;
+  void* ptr = nullptr;
+  hipError_t e = goda::decode_scratch(&ptr);
+  if (e != hipSuccess) return hip_status(e, "decode_noalloc: scratch lookup");
+  b.workspace = ptr;
+  b.workspace_bytes = goda::kDecodeScratchBytes;
+  return hip_status(goda::launch_decode(make_decode_params(b), reinterpret_cast<hipStream_t>(stream)),
+                    "decode_noalloc");
 }
 
 int32_t goda_attn_kv_append(const goda_kv_append_args* a, void* stream) {

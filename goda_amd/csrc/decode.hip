@@ -30,7 +30,38 @@
 #include "common.h"
 #include "launch.h"
 
+// Split-K partials of goda_attn_decode_noalloc: a fixed device-resident array
+// instead of a caller workspace, for callers that cannot allocate. Each GPU
+// holds its own copy for the life of the process; every call on that GPU
+// shares it, so calls that overlap on one GPU race. Nothing in it has to
+// start at zero: the decode kernel writes every partial slot that the merge
+// kernel of the same call reads.
+static __device__ __align__(256) unsigned char scratch[goda::kDecodeScratchBytes];
+
 namespace goda {
+
+hipError_t decode_scratch(void** ptr) {
+  // Host code must never pass `scratch` itself to a kernel (it is a host-side
+  // stand-in, not a device address): its address on each device is looked up
+  // once, with that device current, and kept per device.
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
+}
+
 namespace {
 
 constexpr int kWaves = 4;
@@ -799,11 +830,6 @@ hipError_t launch_append_t(const goda_kv_append_args& a, hipStream_t s) {
 }
 
 }  // namespace
-
-bool decode_mfma_supported(const goda_decode_args& a) {
-  if (a.dtype != GODA_DTYPE_BF16 && a.dtype != GODA_DTYPE_F16 && a.dtype != GODA_DTYPE_F32) return false;
-  return a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256;
-}
 
 int64_t decode_slots(const goda_decode_args& a) {
   // Ranges are at most ceil(total / split), or with the balanced default at

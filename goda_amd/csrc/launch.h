@@ -67,11 +67,19 @@ bool prefill_mfma_supported(const goda_prefill_args& a);
 int64_t prefill_mfma_workspace_bytes(const goda_prefill_args& a);
 hipError_t launch_prefill_mfma(const PrefillParams& p, hipStream_t s);
 
-// Split-K decode for bf16/fp16; fp32 decode goes through the generic prefill.
-bool decode_mfma_supported(const goda_decode_args& a);
+// Split-K decode (bf16 / fp16 / fp32).
 int64_t decode_slots(const goda_decode_args& a);
 int64_t decode_workspace_bytes(const goda_decode_args& a);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s);
+
+// Size of the device-resident scratch array of goda_attn_decode_noalloc: the
+// split-K partials of any decode with the balanced default split
+// (split_size = 0) fit, the largest being head_dim 128 with 16 query heads
+// per workgroup: 2 * 2048 slots * 16 heads * (128 + 1) floats = 33.8 MB.
+constexpr int64_t kDecodeScratchBytes = GODA_DECODE_NOALLOC_SCRATCH_BYTES;
+// Device address of that array on the current device (looked up once per
+// device with hipGetSymbolAddress).
+hipError_t decode_scratch(void** ptr);
 
 hipError_t launch_kv_append(const goda_kv_append_args& a, hipStream_t s);
 

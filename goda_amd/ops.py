@@ -354,6 +354,7 @@ def plan_decode(
     cache_layout: str = "bthd",
     return_lse: bool = False,
     out: torch.Tensor | None = None,
+    noalloc: bool = False,
 ):
     """Validate and prepare a one-token decode over a KV cache with
     per-sequence lengths; returns the `Launch`.
@@ -362,6 +363,9 @@ def plan_decode(
     cache_layout == "bthd" (goda's KVCache, mint/kvcache/base.py:22-31) or
     [B, Hkv, Lmax, D] when "bhtd"; cache_seqlens int32 [B] = valid keys
     (the new token included). The query sits at position cache_seqlens[b]-1.
+    With `noalloc` the launch goes through `goda_attn_decode_noalloc`, whose
+    split-K partials live in the library's fixed device-resident array (no
+    workspace; calls overlapping on one GPU race).
     """
     squeeze = False
     if q.dim() == 4:
@@ -427,12 +431,13 @@ def plan_decode(
     if need < 0:
         _lib.check(int(need))
     ws = None
-    if need > 0:
+    if need > 0 and not noalloc:
         ws = torch.empty(int(need), dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = ws.data_ptr(), int(need)
     ov = o.unsqueeze(1) if squeeze else o
     keep = (q, k_cache, v_cache, seqlens, o, lse, ws, slopes, cos, sin, qn)
-    return Launch("goda_attn_decode", a, keep, (ov, lse) if return_lse else ov)
+    fn = "goda_attn_decode_noalloc" if noalloc else "goda_attn_decode"
+    return Launch(fn, a, keep, (ov, lse) if return_lse else ov)
 
 
 def kv_append(

@@ -261,6 +261,20 @@ int64_t goda_attn_decode_workspace_size(const goda_decode_args* args);
  * flash_attn_with_kvcache call at mint/nn/flashattn.py:191-200. */
 int32_t goda_attn_decode(const goda_decode_args* args, void* stream);
 
+/* goda_attn_decode that allocates nothing and takes no workspace
+ * (args->workspace / workspace_bytes are ignored). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The split-K partials live in a fixed device-resident array of 36 MiB
+ * (GODA_DECODE_NOALLOC_SCRATCH_BYTES) that each GPU holds until the process
+ * ends; every decode with split_size 0 (the balanced default) fits, and a
+ * call whose partials would not fit fails with GODA_ERR_WORKSPACE. All calls
+ * on one GPU share that array: calls that overlap on one GPU (concurrent
+ * streams or threads) race and must be serialised by the caller. Results
+ * equal goda_attn_decode's for the same arguments. */
+#define GODA_DECODE_NOALLOC_SCRATCH_BYTES (36ll << 20)
+int32_t goda_attn_decode_noalloc(const goda_decode_args* args, void* stream);
+
 /* Append seqlen_new rows of k/v to every sequence at its own position
  * cache_seqlens[b] (optionally rotating k), then advance cache_seqlens.
  * Replaces KVCache.update (mint/kvcache/base.py:35-50) without the

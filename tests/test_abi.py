@@ -121,6 +121,41 @@ def test_decode_and_append_reject_bad_arguments(lib):
     assert lib.goda_attn_kv_append(ctypes.byref(k), None) == _lib.ERR_INVALID_ARG
 
 
+def _decode_args(**over):
+    d = _lib.DecodeArgs()
+    d.dtype, d.batch, d.heads_q, d.heads_kv, d.head_dim = _lib.DTYPE_BF16, 1, 8, 8, 128
+    d.max_seqlen, d.softmax_scale = 64, 0.1
+    for k, v in over.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (32, 8), (64, 8), (128, 8), (16, 1), (8, 1)])
+def test_decode_noalloc_scratch_holds_every_balanced_split(lib, d, hq, hkv):
+    """With split_size 0 (the balanced default) the split-K partials of any
+    batch and cache length fit the fixed scratch array of
+    goda_attn_decode_noalloc."""
+    a = _decode_args(batch=4096, heads_q=hq, heads_kv=hkv, head_dim=d, max_seqlen=1 << 20, split_size=0)
+    need = lib.goda_attn_decode_workspace_size(ctypes.byref(a))
+    assert 0 < need <= _lib.DECODE_NOALLOC_SCRATCH_BYTES
+
+
+def test_decode_noalloc_rejects_partials_beyond_the_scratch_array(lib):
+    """A fixed small split over a long cache needs more partial slots than
+    the scratch array holds: the call fails before any GPU work (the tensor
+    pointers here are never dereferenced)."""
+    a = _decode_args(heads_q=128, heads_kv=8, max_seqlen=65536, split_size=64)
+    a.q = a.k_cache = a.v_cache = a.o = a.cache_seqlens = 256
+    need = lib.goda_attn_decode_workspace_size(ctypes.byref(a))
+    assert need > _lib.DECODE_NOALLOC_SCRATCH_BYTES
+    assert lib.goda_attn_decode_noalloc(ctypes.byref(a), None) == _lib.ERR_WORKSPACE
+    assert "scratch" in lib.goda_attn_last_error().decode()
+    # argument checks come first, as in goda_attn_decode
+    a.split_size = 100
+    assert lib.goda_attn_decode_noalloc(ctypes.byref(a), None) == _lib.ERR_INVALID_ARG
+
+
 def test_empty_batch_is_a_no_op(lib):
     a = _prefill_args(batch=0)
     assert lib.goda_attn_prefill_fwd(ctypes.byref(a), None) == _lib.OK
