@@ -17,7 +17,7 @@ from pathlib import Path
 _LIB_ENV = "GODA_ATTN_LIB"
 _DEFAULT = Path(__file__).resolve().parent / "lib" / "libgoda_attn.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -81,8 +81,13 @@ class PrefillArgs(ctypes.Structure):
         ("rope_q_offset", _i32),
         ("rope_k_offset", _i32),
         ("norm_eps", _f32),
+        ("rope_pos_abs", _i32),
         ("q_norm_weight", _vp),
         ("k_norm_weight", _vp),
+        ("mask_bits", _vp),
+        ("mask_stride_b", _i64),
+        ("mask_stride_h", _i64),
+        ("mask_stride_q", _i64),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
         ("timing_begin", _vp),
@@ -101,7 +106,7 @@ class DecodeArgs(ctypes.Structure):
         ("window_left", _i32),
         ("split_size", _i32),
         ("softmax_scale", _f32),
-        ("reserved0", _i32),
+        ("rope_pos_abs", _i32),
         ("q", _vp),
         ("q_stride_b", _i64),
         ("q_stride_h", _i64),
@@ -166,6 +171,9 @@ class KvAppendArgs(ctypes.Structure):
         ("rope_k_offset", _i32),
         ("norm_eps", _f32),
         ("k_norm_weight", _vp),
+        ("rope_pos_abs", _i32),
+        ("reserved0", _i32),
+        ("status", _vp),
     ]
 
 

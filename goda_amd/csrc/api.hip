@@ -69,8 +69,9 @@ int32_t check_prefill(const goda_prefill_args* a, bool need_ptrs) {
     if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
       return fail(GODA_ERR_INVALID_ARG, "prefill: RoPE requested without cos/sin tables");
     // Highest position touched: q rows sit at rope_q_offset + (Lk - Lq) + i <=
-    // rope_q_offset + seqlen_k - 1 when Lq >= 1; k rows at rope_k_offset + j.
-    const int64_t qmax = (int64_t)a->rope_q_offset + a->seqlen_k - 1;
+    // rope_q_offset + seqlen_k - 1 when Lq >= 1 (rope_pos_abs: at
+    // rope_q_offset + i); k rows at rope_k_offset + j.
+    const int64_t qmax = (int64_t)a->rope_q_offset + (a->rope_pos_abs ? a->seqlen_q : a->seqlen_k) - 1;
     const int64_t kmax = (int64_t)a->rope_k_offset + a->seqlen_k - 1;
     if (a->rope_q && (a->rope_q_offset < 0 || qmax >= a->rope_len))
       return fail(GODA_ERR_INVALID_ARG, "prefill: q positions up to %lld exceed rope_len %d",
@@ -78,8 +79,16 @@ int32_t check_prefill(const goda_prefill_args* a, bool need_ptrs) {
     if (a->rope_k && (a->rope_k_offset < 0 || kmax >= a->rope_len))
       return fail(GODA_ERR_INVALID_ARG, "prefill: k positions up to %lld exceed rope_len %d",
                   (long long)kmax, a->rope_len);
-    if (a->rope_q && !a->cu_seqlens_q && a->seqlen_q > a->seqlen_k && !a->seqused_k)
+    if (a->rope_q && !a->rope_pos_abs && !a->cu_seqlens_q && a->seqlen_q > a->seqlen_k && !a->seqused_k)
       return fail(GODA_ERR_INVALID_ARG, "prefill: RoPE on q needs seqlen_q <= seqlen_k");
+  }
+  if (a->mask_bits) {
+    if (a->cu_seqlens_q)
+      return fail(GODA_ERR_UNSUPPORTED, "prefill: a mask needs a dense launch (cu_seqlens NULL)");
+    if ((reinterpret_cast<uintptr_t>(a->mask_bits) & 7) != 0 || (a->mask_stride_b & 1) || (a->mask_stride_h & 1) ||
+        (a->mask_stride_q & 1) || a->mask_stride_b < 0 || a->mask_stride_h < 0 || a->mask_stride_q < 0)
+      return fail(GODA_ERR_INVALID_ARG,
+                  "prefill: mask_bits must be 8-byte aligned with even, non-negative word strides");
   }
   return GODA_OK;
 }
@@ -119,9 +128,10 @@ int32_t check_decode(const goda_decode_args* a) {
   if (a->rope_q) {
     if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
       return fail(GODA_ERR_INVALID_ARG, "decode: RoPE requested without cos/sin tables");
-    if (a->rope_q_offset < 0 || (int64_t)a->rope_q_offset + a->max_seqlen - 1 >= a->rope_len)
-      return fail(GODA_ERR_INVALID_ARG, "decode: q positions up to %lld exceed rope_len %d",
-                  (long long)a->rope_q_offset + a->max_seqlen - 1, a->rope_len);
+    const int64_t qmax = (int64_t)a->rope_q_offset + (a->rope_pos_abs ? 0 : a->max_seqlen - 1);
+    if (a->rope_q_offset < 0 || qmax >= a->rope_len)
+      return fail(GODA_ERR_INVALID_ARG, "decode: q positions up to %lld exceed rope_len %d", (long long)qmax,
+                  a->rope_len);
   }
   return GODA_OK;
 }
@@ -260,9 +270,10 @@ int32_t goda_attn_kv_append(const goda_kv_append_args* a, void* stream) {
   if (a->rope_k) {
     if (!a->rope_cos || !a->rope_sin || a->rope_len <= 0)
       return fail(GODA_ERR_INVALID_ARG, "kv_append: RoPE requested without cos/sin tables");
-    if (a->rope_k_offset < 0 || (int64_t)a->rope_k_offset + a->max_seqlen - 1 >= a->rope_len)
-      return fail(GODA_ERR_INVALID_ARG, "kv_append: positions up to %lld exceed rope_len %d",
-                  (long long)a->rope_k_offset + a->max_seqlen - 1, a->rope_len);
+    const int64_t kmax = (int64_t)a->rope_k_offset + (a->rope_pos_abs ? a->seqlen_new : a->max_seqlen) - 1;
+    if (a->rope_k_offset < 0 || kmax >= a->rope_len)
+      return fail(GODA_ERR_INVALID_ARG, "kv_append: positions up to %lld exceed rope_len %d", (long long)kmax,
+                  a->rope_len);
   }
   return hip_status(goda::launch_kv_append(*a, reinterpret_cast<hipStream_t>(stream)), "kv_append");
 }

@@ -3,11 +3,10 @@
 // quantities: D = rowsum(dO * O), P = exp(scale * q k^T - M),
 // dV = P^T dO, dS = P * (dO V^T - D), dQ = scale * dS K, dK = scale * dS^T Q).
 //
-// This file holds the row-statistics pre-pass and the generic kernels: fp32
-// arithmetic on the vector ALUs for every dtype and head_dim in {64, 128,
-// 256} (the fp32 training path; goda's default model dtype is fp32,
-// mint/nn/models.py:23); bf16/fp16 with head_dim 64 or 128 run on the matrix
-// cores instead (backward_mfma.hip). Three launches:
+// This file holds the generic kernels: fp32 arithmetic on the vector ALUs,
+// the path for fp32 at head_dim 256 (goda's default model dtype is fp32,
+// mint/nn/models.py:23), whose operands do not fit the matrix-core kernels;
+// every other dtype / head_dim runs on backward_mfma.hip. Three launches:
 //   1. bwd_delta_kernel   delta[hq][row] = sum_d dO * O (fp32 workspace);
 //   2. bwd_dkv_kernel     one workgroup per (key block, KV head, sequence):
 //                         keys stay in registers, query rows of every head of
@@ -229,7 +228,7 @@ __global__ void __launch_bounds__(kThreads) bwd_dkv_kernel(const BwdParams p) {
           load4f<T>(dr + c4, g1);
           load4f<T>(dr + c4 + D / 2, g2);
           if (a.rope_q) {
-            const int pos = min(max(a.rope_q_offset + diag + i, 0), a.rope_len - 1);
+            const int pos = rope_qpos(a, diag, i);
             const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c4;
             const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c4;
 #pragma unroll
@@ -267,6 +266,7 @@ __global__ void __launch_bounds__(kThreads) bwd_dkv_kernel(const BwdParams p) {
         bool vis = key_valid && i < i_hi && Ls[ir] != kNegInf;
         if (a.causal) vis = vis && j <= iabs;
         if (use_window) vis = vis && iabs - j <= a.window_left;
+        if (vis && a.mask_bits) vis = mask_bit(mask_row(a, b, hq, i), j);
         float t = s * c;
         if (a.alibi_slopes) t = fmaf(slope2, (float)(j - iabs), t);
         const float pr = vis ? exp2f(t - Ls[ir]) : 0.f;
@@ -321,7 +321,7 @@ __global__ void __launch_bounds__(kThreads) bwd_dq_kernel(const BwdParams p) {
   float l2 = kNegInf, dl = 0.f;
 #pragma unroll
   for (int e = 0; e < 32; ++e) q[e] = d_o[e] = dq[e] = 0.f;
-  const int qpos = row_valid ? min(max(a.rope_q_offset + iabs, 0), a.rope_len - 1) : 0;
+  const int qpos = row_valid ? rope_qpos(a, diag, i) : 0;
   if (row_valid) {
     load_part<T, D>(row_ptr<T>(a.q, a.q_stride_b, a.q_stride_t, a.q_stride_h, varlen, b, g.q_row0 + i, hq), part, q);
     load_part<T, D>(row_ptr<T>(gr.d_o, gr.do_stride_b, gr.do_stride_t, gr.do_stride_h, varlen, b, g.q_row0 + i, hq),
@@ -385,6 +385,7 @@ __global__ void __launch_bounds__(kThreads) bwd_dq_kernel(const BwdParams p) {
       bool vis = row_valid && j < kv_hi && l2 != kNegInf;
       if (a.causal) vis = vis && j <= iabs;
       if (use_window) vis = vis && iabs - j <= a.window_left;
+      if (vis && a.mask_bits) vis = mask_bit(mask_row(a, b, hq, i), j);
       float t = s * c;
       if (a.alibi_slopes) t = fmaf(slope2, (float)(j - iabs), t);
       const float pr = vis ? exp2f(t - l2) : 0.f;

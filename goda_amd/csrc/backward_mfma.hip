@@ -1,5 +1,6 @@
-// Backward of prefill attention on gfx950 matrix cores: bf16 / fp16 operands,
-// fp32 accumulation, head_dim 64, 128 or 256 (others take the generic kernels).
+// Backward of prefill attention on gfx950 matrix cores: bf16 / fp16 operands
+// at head_dim 64, 128 or 256, fp32 operands at head_dim 64 or 128 (fp32 at 256
+// takes the generic kernels of backward.hip); fp32 accumulation.
 // Same quantities as kernels_/flash_attn_gqa/cuda.py:6-246:
 //   P = exp(scale q k^T + bias - lse), dV = P^T dO, dP = dO V^T,
 //   dS = P * (dP - delta) with delta = rowsum(dO * O),
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
       g1 = ld_vec<v8>(gr + c);
       g2 = ld_vec<v8>(gr + c + D / 2);
       if (a.rope_q) {
-        const int pos = min(max(a.rope_q_offset + diag + i, 0), a.rope_len - 1);
+        const int pos = rope_qpos(a, diag, i);
         const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
         const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
 #pragma unroll
@@ -264,6 +265,35 @@ __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
   }
 }
 
+// Key-major copy of the caller's row-major mask bits, for the dk/dv kernels
+// (a lane there holds one key and 16 query rows of a 32-row tile): word
+// [b][h][key][query tile] bit r = row 32 * tile + r. A thread reads the 32
+// row words of one (query tile, 32-key word), transposes the 32x32 bit block
+// in registers and writes the 32 key words.
+__global__ void __launch_bounds__(256) bwd_mask_t_kernel(const BwdParams p) {
+  const goda_prefill_args& a = p.a;
+  const int nkw = (a.seqlen_k + 31) / 32;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.ntq * nkw) return;
+  const int qt = (int)(idx % p.ntq), kw = (int)(idx / p.ntq);
+  const int hm = blockIdx.y, bm = blockIdx.z;
+  uint32_t m[32];
+#pragma unroll
+  for (int r = 0; r < 32; ++r) {
+    const int i = 32 * qt + r;
+    m[r] = i < a.seqlen_q ? mask_row(a, bm, hm, i)[kw] : 0u;
+  }
+  uint32_t* out = p.mask_t + bm * p.mt_stride_b + hm * p.mt_stride_h;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int r = 0; r < 32; ++r) w |= ((m[r] >> c) & 1u) << r;
+    const int key = 32 * kw + c;
+    if (key < a.seqlen_k) out[(int64_t)key * p.ntq + qt] = w;
+  }
+}
+
 // Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
 // run LEAD MFMAs ahead (not all hoisted, which would hold 4 registers each).
 template <typename T, int NM, int LEAD>
@@ -337,7 +367,7 @@ __device__ __forceinline__ void chunked_order_3d(int& bx, int& by, int& bz) {
   bz = unit / (int)gridDim.y;
 }
 
-template <typename T, int D, bool ALIBI>
+template <typename T, int D, bool ALIBI, bool MASK>
 __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
@@ -432,6 +462,10 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         const int q0 = (qt_lo + it % nq) * kQRows;
         const v8* st = stage(it);
         const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
+        // The caller's mask bits of this key for the tile's 32 rows.
+        uint32_t mword = 0;
+        if (MASK && key_ok)
+          mword = p.mask_t[b * p.mt_stride_b + hq * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo + it % nq] >> (4 * hi);
         // S [rows][keys] and dP: two interleaved accumulation chains.
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -462,6 +496,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
             if (ALIBI) t += base - slope2 * (float)off;
             float pv = fast_exp2(t - l2[e]);
             if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+            if (MASK) pv = keep_if_bit(pv, mword, off, 0.f);
             pr[r] = pv;
             ds[r] = pv * (dp[r] - dl[e]);
           }
@@ -552,7 +587,7 @@ constexpr int kWavesWide = 4;
 constexpr int kWideParts = 4;
 
 
-template <typename T, int D, bool ALIBI>
+template <typename T, int D, bool ALIBI, bool MASK>
 __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const BwdParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
@@ -663,6 +698,10 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     };
 
     load_part(nx, 0);
+    // The caller's mask bits of this key for the tile's 32 rows.
+    uint32_t mword = 0;
+    if (MASK && key < g.lk)
+      mword = p.mask_t[b * p.mt_stride_b + hq * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo + it % nq] >> (4 * hi);
     // S and dP: two independent accumulation chains, interleaved.
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -696,6 +735,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
         if (ALIBI) t += base - slope2 * (float)off;
         float pv = fast_exp2(t - l2[e]);
         if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+        if (MASK) pv = keep_if_bit(pv, mword, off, 0.f);
         pr[r] = pv;
         ds[r] = pv * (dp[r] - dl[e]);
       }
@@ -823,7 +863,7 @@ __global__ void __launch_bounds__(256) bwd_dkv_reduce_kernel(const BwdParams p) 
 // ---------------------------------------------------------------------------
 // 4. dq
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool ALIBI>
+template <typename T, int D, bool ALIBI, bool MASK>
 __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::OCC)) bwd_dq_mfma_kernel(const BwdParams p) {
   constexpr int kWavesDq = DqShape<T, D>::WAVES;
   typedef typename Vec<T>::v8 v8;
@@ -887,6 +927,9 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
   }
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
   const float c = p.scale_log2;
+  // The caller's mask row of this lane's query row (rows past the sequence
+  // read the last row's bits and are masked anyway): one word per key tile.
+  const uint32_t* mrow = MASK ? mask_row(a, b, hq, min(i, g.lq - 1)) : nullptr;
 
   // key tiles visible to some row of the workgroup
   const int q_last = min(qr0 + qb_rows, g.lq) - 1;
@@ -916,9 +959,11 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
       if (KI::CHUNKS % (kWavesDq * 64) == 0 || tid + x * kWavesDq * 64 < KI::CHUNKS) dst[tid + x * kWavesDq * 64] = stg[x];
   };
 
+  static_assert(kBKV == 32, "one mask word per key tile");
   auto compute = [&](int it) {
     const int kvb = (j_lo + it) * kBKV;
     const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * KI::BYTES);
+    const uint32_t mword = MASK ? mrow[j_lo + it] >> (4 * hi) : 0u;
     // S^T[keys][rows] and dP^T
     f32x16 s[MT], dp[MT];
 #pragma unroll
@@ -950,6 +995,7 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
         if (ALIBI) t += base + slope2 * (float)off;
         float pv = fast_exp2(t - l2);
         if (need_mask) pv = (row_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
+        if (MASK) pv = keep_if_bit(pv, mword, off, 0.f);
         ds[r] = pv * (dp[mt][r] - dl);
       }
       dsf[2 * mt] = pack8<v8, T>(ds);
@@ -982,7 +1028,7 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
 #pragma unroll
   for (int md = 0; md < MD; ++md) dq[md] *= a.softmax_scale;
   if (a.rope_q) {
-    const int pos = min(max(a.rope_q_offset + iabs, 0), a.rope_len - 1);
+    const int pos = rope_qpos(a, diag, i);
 #pragma unroll
     for (int md = 0; md < MD / 2; ++md)
 #pragma unroll
@@ -1015,14 +1061,14 @@ int gcd_int(int x, int y) {
   return x;
 }
 
-template <typename T, int D, bool ALIBI>
+template <typename T, int D, bool ALIBI, bool MASK>
 hipError_t launch_main(const BwdParams& p, hipStream_t s) {
   const goda_prefill_args& a = p.a;
   hipError_t e;
   if ((e = record_timing(p.g.timing_begin, s)) != hipSuccess) return e;
   if (a.seqlen_k > 0) {
     if constexpr (DqShape<T, D>::WIDE) {
-      auto kern = bwd_dkv_wide_kernel<T, D, ALIBI>;
+      auto kern = bwd_dkv_wide_kernel<T, D, ALIBI, MASK>;
       const size_t lds = 2 * (size_t)QImg<T, D>::BYTES;
       if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
         return e;
@@ -1035,7 +1081,7 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
         if ((e = hipGetLastError()) != hipSuccess) return e;
       }
     } else {
-      auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI>;
+      auto kern = bwd_dkv_mfma_kernel<T, D, ALIBI, MASK>;
       const size_t lds = (size_t)DkvSmem<T, D>::BYTES;
       if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
         return e;
@@ -1045,7 +1091,7 @@ hipError_t launch_main(const BwdParams& p, hipStream_t s) {
     }
   }
   if (a.seqlen_q > 0) {
-    auto kern = bwd_dq_mfma_kernel<T, D, ALIBI>;
+    auto kern = bwd_dq_mfma_kernel<T, D, ALIBI, MASK>;
     const size_t lds = 2 * (size_t)KVImg<T, D>::BYTES;
     if ((e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)) != hipSuccess)
       return e;
@@ -1074,6 +1120,15 @@ int dkv_splits(const goda_prefill_args& a) {
   return (int)std::min<int64_t>(ns, 8);
 }
 
+// Key-major mask words: (batches, heads) of the mask (1 where it broadcasts)
+// x keys x query tiles.
+int64_t mask_t_words(const goda_prefill_args& a) {
+  if (!a.mask_bits) return 0;
+  const int64_t bm = a.mask_stride_b ? a.batch : 1, hm = a.mask_stride_h ? a.heads_q : 1;
+  return bm * hm * a.seqlen_k * ((a.seqlen_q + kQRows - 1) / kQRows);
+}
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
 template <typename T, int D>
 int64_t workspace_bytes_d(const goda_prefill_args& a) {
   const int64_t ntq = (a.seqlen_q + kQRows - 1) / kQRows;
@@ -1081,6 +1136,7 @@ int64_t workspace_bytes_d(const goda_prefill_args& a) {
   int64_t bytes = (int64_t)a.batch * (ntq * a.heads_q * QImg<T, D>::BYTES + ntk * a.heads_kv * KVImg<T, D>::BYTES);
   const int ns = dkv_splits(a);
   if (ns > 1) bytes += (int64_t)ns * 2 * a.batch * a.seqlen_k * a.heads_kv * D * 4;
+  if (a.mask_bits) bytes = align256(bytes) + 4 * mask_t_words(a);
   return bytes;
 }
 
@@ -1095,6 +1151,20 @@ hipError_t launch_d(BwdParams p, hipStream_t s) {
   p.nsplit = dkv_splits(a);
   p.part = reinterpret_cast<float*>(p.kvimg + (int64_t)a.batch * p.ntk * a.heads_kv * KVImg<T, D>::BYTES);
   hipError_t e;
+  if (a.mask_bits) {
+    int64_t off = (int64_t)(reinterpret_cast<unsigned char*>(p.part) - p.qimg);
+    if (p.nsplit > 1) off += (int64_t)p.nsplit * 2 * a.batch * a.seqlen_k * a.heads_kv * D * 4;
+    p.mask_t = reinterpret_cast<uint32_t*>(p.qimg + align256(off));
+    const int64_t hm = a.mask_stride_h ? a.heads_q : 1;
+    p.mt_stride_h = a.mask_stride_h ? (int64_t)a.seqlen_k * p.ntq : 0;
+    p.mt_stride_b = a.mask_stride_b ? hm * a.seqlen_k * p.ntq : 0;
+    const int64_t threads = (int64_t)p.ntq * ((a.seqlen_k + 31) / 32);
+    if (threads > 0) {
+      const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)hm, a.mask_stride_b ? a.batch : 1);
+      bwd_mask_t_kernel<<<grid, 256, 0, s>>>(p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+  }
   if (p.ntq > 0) {
     pack_q_bwd_kernel<T, D><<<dim3(p.ntq, a.heads_q, a.batch), 256, 0, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1103,8 +1173,9 @@ hipError_t launch_d(BwdParams p, hipStream_t s) {
     pack_kv_bwd_kernel<T, D><<<dim3(p.ntk, a.heads_kv, a.batch), 256, 0, s>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (a.alibi_slopes) return launch_main<T, D, true>(p, s);
-  return launch_main<T, D, false>(p, s);
+  if (a.mask_bits)
+    return a.alibi_slopes ? launch_main<T, D, true, true>(p, s) : launch_main<T, D, false, true>(p, s);
+  return a.alibi_slopes ? launch_main<T, D, true, false>(p, s) : launch_main<T, D, false, false>(p, s);
 }
 
 template <typename T>

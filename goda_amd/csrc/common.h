@@ -164,4 +164,25 @@ __device__ __forceinline__ SeqGeom seq_geom(int b, int seqlen_q, int seqlen_k,
   return g;
 }
 
+// RoPE position of query row i (0-based within its sequence; diag = Lk - Lq):
+// rope_q_offset + diag + i, or rope_q_offset + i with rope_pos_abs (a
+// caller-given start position), clamped into the table the host validated.
+__device__ __forceinline__ int rope_qpos(const goda_prefill_args& a, int diag, int i) {
+  return min(max(a.rope_q_offset + (a.rope_pos_abs ? 0 : diag) + i, 0), a.rope_len - 1);
+}
+
+// Row (b, query head h, query row i) of the bit-packed mask: bit j % 32 of
+// word j / 32 is key j's visibility.
+__device__ __forceinline__ const uint32_t* mask_row(const goda_prefill_args& a, int b, int h, int i) {
+  return a.mask_bits + (int64_t)b * a.mask_stride_b + (int64_t)h * a.mask_stride_h + (int64_t)i * a.mask_stride_q;
+}
+__device__ __forceinline__ bool mask_bit(const uint32_t* row, int j) { return (row[j >> 5] >> (j & 31)) & 1u; }
+
+// Keep `x` where the 1-bit field `bit` of `w` is set, else `repl`: one
+// bit-field extract (0 or all ones) and one bit-field select, no compare.
+__device__ __forceinline__ float keep_if_bit(float x, uint32_t w, int bit, float repl) {
+  const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int)w, bit, 1);
+  return __uint_as_float((__float_as_uint(x) & sel) | (__float_as_uint(repl) & ~sel));
+}
+
 }  // namespace goda

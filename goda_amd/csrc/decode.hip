@@ -329,7 +329,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
         }
       }
       if (a.rope_q && head_ok) {
-        const int pos = qpos + a.rope_q_offset;
+        const int pos = (a.rope_pos_abs ? 0 : qpos) + a.rope_q_offset;
 #pragma unroll
         for (int ks = 0; ks < KS / 2; ++ks) {
           const int f0 = 32 * ks + 8 * kg;
@@ -759,7 +759,7 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const goda_kv_append_arg
   const T* vn = reinterpret_cast<const T*>(a.v_new) + (int64_t)b * a.vn_stride_b + (int64_t)t * a.vn_stride_t;
   T* kc = reinterpret_cast<T*>(a.k_cache) + (int64_t)b * a.k_stride_b + (int64_t)pos * a.k_stride_t;
   T* vc = reinterpret_cast<T*>(a.v_cache) + (int64_t)b * a.v_stride_b + (int64_t)pos * a.v_stride_t;
-  const int rp = pos + a.rope_k_offset;
+  const int rp = (a.rope_pos_abs ? t : pos) + a.rope_k_offset;
   for (int h = threadIdx.x >> 6; h < a.heads_kv; h += 4) {
     float x[M];
 #pragma unroll
@@ -800,9 +800,16 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const goda_kv_append_arg
   }
 }
 
-__global__ void kv_bump_kernel(int32_t* seqlens, int n, int add) {
+// Advances the lengths by `add`, clamped to [0, lmax]: a sequence that would
+// pass the end keeps the rows that fit (kv_append_kernel drops the others),
+// and the overflow is reported through `status` instead of being silent.
+__global__ void kv_bump_kernel(int32_t* seqlens, int n, int add, int lmax, int32_t* status) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b < n) seqlens[b] += add;
+  if (b >= n) return;
+  const int64_t len = (int64_t)seqlens[b] + add;
+  const bool bad = len > lmax || len < 0;
+  seqlens[b] = (int32_t)(len > lmax ? lmax : len < 0 ? 0 : len);
+  if (bad && status) *status = 1;
 }
 
 template <typename T>
@@ -825,7 +832,8 @@ hipError_t launch_append_t(const goda_kv_append_args& a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  kv_bump_kernel<<<(a.batch + 255) / 256, 256, 0, s>>>(a.cache_seqlens, a.batch, a.seqlen_new);
+  kv_bump_kernel<<<(a.batch + 255) / 256, 256, 0, s>>>(a.cache_seqlens, a.batch, a.seqlen_new, a.max_seqlen,
+                                                        a.status);
   return hipGetLastError();
 }
 

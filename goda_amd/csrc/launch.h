@@ -48,6 +48,11 @@ struct BwdParams {
   // partials [nsplit][dk, dv][batch * seqlen_k][heads_kv][head_dim] here.
   int nsplit;
   float* part;
+  // Caller's mask, key-major for the dk/dv kernels (whose lanes hold keys):
+  // word [b][h][key][query tile] holds bit r for query row 32*tile + r.
+  // Broadcast dimensions of the mask keep a zero stride.
+  uint32_t* mask_t;
+  int64_t mt_stride_b, mt_stride_h;
 };
 
 // Backward: workspace bytes and the launch (generic VALU kernels for every

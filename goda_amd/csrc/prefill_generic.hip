@@ -1,8 +1,8 @@
-// Generic prefill attention on the vector ALUs: every dtype (fp32 / fp16 /
-// bf16) and head_dim in {64, 128, 256}. It is the fp32 product path (goda's
-// default model dtype is fp32, mint/nn/models.py:23) and the path for the
-// one-token fp32 decode. Arithmetic is fp32 throughout, so fp32 inputs keep
-// full precision.
+// Generic prefill attention on the vector ALUs, fp32 arithmetic throughout.
+// The product path for fp32 at head_dim 256 (goda's default model dtype is
+// fp32, mint/nn/models.py:23), whose operands do not fit the matrix-core
+// kernel's register and LDS budgets; every other dtype / head_dim runs on
+// prefill_mfma.hip.
 //
 // Work split: one workgroup of 256 threads per (64-query block, query head,
 // sequence). Four threads share a query row; thread `part` owns head-dim
@@ -91,7 +91,7 @@ prefill_generic_kernel(const PrefillParams p) {
         for (int j = 0; j < 4; ++j) q[4 * gi + j] *= inv * (1.f + a.q_norm_weight[16 * gi + 4 * part + j]);
     }
     if (a.rope_q) {
-      const int pos = min(max(a.rope_q_offset + diag + i, 0), a.rope_len - 1);
+      const int pos = rope_qpos(a, diag, i);
       const float* cs = a.rope_cos + (int64_t)pos * (D / 2);
       const float* sn = a.rope_sin + (int64_t)pos * (D / 2);
 #pragma unroll
@@ -113,6 +113,7 @@ prefill_generic_kernel(const PrefillParams p) {
 
   const float slope_log2 = a.alibi_slopes ? a.alibi_slopes[hq] * kLog2e : 0.f;
   const int iabs = diag + i;  // absolute position of this query
+  const uint32_t* mrow = a.mask_bits ? mask_row(a, b, hq, row_valid ? i : 0) : nullptr;
 
   // ---- key range of the workgroup ----------------------------------------
   const int i_last = min(q0 + kRows, g.lq) - 1;
@@ -211,6 +212,7 @@ prefill_generic_kernel(const PrefillParams p) {
       bool vis = row_valid && j < g.lk && j >= kv_lo;
       if (a.causal) vis = vis && (j <= iabs);
       if (use_window) vis = vis && (iabs - j <= a.window_left);
+      if (vis && mrow) vis = mask_bit(mrow, j);
       float t = s * p.scale_log2;
       if (a.alibi_slopes) t = fmaf(slope_log2, (float)(j - iabs), t);
       x[jr] = vis ? t : kNegInf;

@@ -279,7 +279,22 @@ __device__ __forceinline__ float dot2_ones(f16x8 p, int i, float acc) {
   return __builtin_amdgcn_fdot2(v, one, acc, false);
 }
 
-template <typename T, int D, int BKV, int NT, int WAVES, bool ALIBI>
+// Bits of the caller's boolean mask for one key tile of one query row: 64
+// keys in one 8-byte word, 32 in a 4-byte one.
+template <int BKV>
+struct MaskWord;
+template <>
+struct MaskWord<64> {
+  typedef uint64_t t;
+  static constexpr t kAll = ~0ull;
+};
+template <>
+struct MaskWord<32> {
+  typedef uint32_t t;
+  static constexpr t kAll = ~0u;
+};
+
+template <typename T, int D, int BKV, int NT, int WAVES, bool ALIBI, bool MASK>
 __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const PrefillParams p) {
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
@@ -397,7 +412,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
             }
           }
           if (a.rope_q) {
-            const int pos = min(max(a.rope_q_offset + diag + qi, 0), a.rope_len - 1);
+            const int pos = rope_qpos(a, diag, qi);
 #pragma unroll
             for (int ks = 0; ks < KS / 2; ++ks) {
               const int f0 = 16 * ks + 8 * hi;
@@ -457,6 +472,20 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
   const float alibi_s1 = slope2, alibi_s2 = 2.f * slope2, alibi_s3 = 3.f * slope2, alibi_s8 = 8.f * slope2;
 
+  // Caller's mask: this lane's query rows (rows past the sequence read the
+  // last row's bits, and are never stored). A tile's word is loaded with the
+  // tile's score products and applied in its softmax phase.
+  typedef typename MaskWord<BKV>::t mword_t;
+  const mword_t* mrow[NT];
+  mword_t mw[NT];
+  if constexpr (MASK) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      mrow[nt] = reinterpret_cast<const mword_t*>(mask_row(a, b, hq, min(wrow0 + 32 * nt + l32, g.lq - 1)));
+      mw[nt] = MaskWord<BKV>::kAll;
+    }
+  }
+
   // ---- tile ring ----------------------------------------------------------------
   // Lane chunk c of this wave's share sits at the same offset in the
   // workspace tile and in the LDS stage.
@@ -496,6 +525,10 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // accumulators start at -m (plus the ALiBi bias slope*(kv - i) of each
   // register), so a score leaves the MFMA as the exponent of its P.
   auto qk = [&](int j, f32x16 (&s)[MT][NT]) {
+    if constexpr (MASK) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) mw[nt] = mrow[nt][j];
+    }
     const v8* kp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES) + hi * BKV + l32;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -553,6 +586,24 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
             const int off = 32 * mt + 8 * (r >> 2) + (r & 3);
             s[mt][nt][r] = (off >= lo_lim && off <= hi_lim) ? s[mt][nt][r] : kNegInf;
           }
+      }
+    }
+    if constexpr (MASK) {
+      // Register (mt, r) holds key kvb + 4 hi + 32 mt + 8 (r/4) + r%4.
+      bool partial = false;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) partial = partial || (mw[nt] != MaskWord<BKV>::kAll);
+      if (__builtin_amdgcn_ballot_w64(partial) != 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const mword_t w = mw[nt] >> (4 * hi);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const uint32_t w32 = (uint32_t)(w >> (32 * mt));
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[mt][nt][r] = keep_if_bit(s[mt][nt][r], w32, 8 * (r >> 2) + (r & 3), kNegInf);
+          }
+        }
       }
     }
     // row max (absolute, log2 units) and lazy rescale
@@ -769,7 +820,7 @@ int gcd_int(int x, int y) {
   return x;
 }
 
-template <typename T, int D, bool ALIBI>
+template <typename T, int D, bool ALIBI, bool MASK>
 hipError_t launch_attn(PrefillParams p, hipStream_t s) {
   typedef Config<T, D> C;
   const goda_prefill_args& a = p.a;
@@ -783,7 +834,7 @@ hipError_t launch_attn(PrefillParams p, hipStream_t s) {
   if (nblk <= 0) return hipSuccess;
   if (nblk > 0x7fffffff) return hipErrorInvalidValue;
   const size_t lds = (size_t)kStages * TileGeom<T, D, C::BKV, C::WAVES>::BYTES;
-  auto kern = prefill_fa_kernel<T, D, C::BKV, C::NT, C::WAVES, ALIBI>;
+  auto kern = prefill_fa_kernel<T, D, C::BKV, C::NT, C::WAVES, ALIBI, MASK>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
@@ -805,8 +856,8 @@ hipError_t launch_d(PrefillParams p, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (a.alibi_slopes) return launch_attn<T, D, true>(p, s);
-  return launch_attn<T, D, false>(p, s);
+  if (a.mask_bits) return a.alibi_slopes ? launch_attn<T, D, true, true>(p, s) : launch_attn<T, D, false, true>(p, s);
+  return a.alibi_slopes ? launch_attn<T, D, true, false>(p, s) : launch_attn<T, D, false, false>(p, s);
 }
 
 template <typename T>

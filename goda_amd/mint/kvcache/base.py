@@ -10,9 +10,21 @@ are strided views of it in goda's shape: a decode step then streams each
 5.32 TB/s with the keys of all heads interleaved). Every kernel here takes
 strides, and slicing / element assignment behave as on the reference's
 tensors; code that needs a contiguous tensor calls `.contiguous()`.
-One addition: `append(k, v)` writes every sequence at its OWN current length,
-read on the device (no host sync), which is what ragged decoding needs;
-`update(k, v, start_pos)` keeps the reference's batch-uniform semantics.
+
+Additions:
+  - `append(k, v)` writes every sequence at its OWN current length, read on
+    the device (no host sync), which is what ragged decoding needs;
+    `update(k, v, start_pos)` keeps the reference's batch-uniform semantics.
+  - Overflow is loud, as the reference's slice assignment is
+    (mint/kvcache/base.py:40-43): while the lengths are known on the host
+    (they only changed through this class), an append past `max_seq_len`
+    raises before anything is written; otherwise the kernel keeps the rows
+    that fit, stops the length at `max_seq_len` and sets a device status word
+    that `check()` (and `get()`) turn into an error.
+  - `len_bound` is a host-side upper bound of every sequence's length (None
+    once the caller had the raw tensors, `get_cache_tensors()`, and could
+    have changed them); attention over the cache sizes its launch by it
+    instead of by `max_seq_len`.
 """
 
 from __future__ import annotations
@@ -42,6 +54,8 @@ class KVCache:
         self.k_cache = torch.zeros(store, dtype=dtype, device=device).transpose(1, 2)
         self.v_cache = torch.zeros(store, dtype=dtype, device=device).transpose(1, 2)
         self.cache_seqlens = torch.zeros(max_batch_size, dtype=torch.int32, device=device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=device)
+        self.len_bound: int | None = 0
 
     def append(
         self,
@@ -50,14 +64,24 @@ class KVCache:
         *,
         rope_cos: torch.Tensor | None = None,
         rope_sin: torch.Tensor | None = None,
+        start_pos: int | None = None,
         k_norm_weight: torch.Tensor | None = None,
         norm_eps: float = 1e-6,
     ) -> None:
         """Write k/v [B, T, Hkv, D] at rows cache_seqlens[b] .. +T-1 of each
         sequence b and advance cache_seqlens[:B] by T, all on the device. With
-        RoPE tables, k is rotated at its absolute cache position on the way in
-        (goda caches post-RoPE keys, mint/nn/attn.py:60); with k_norm_weight it
-        is first RMS-normalised like goda's k_norm (mint/nn/attn.py:58)."""
+        RoPE tables, k is rotated on the way in (goda caches post-RoPE keys,
+        mint/nn/attn.py:60): row t at `start_pos + t` when a start position is
+        given (goda's RoPE(q, k, start_pos), mint/nn/pos.py:100-112), else at
+        its own cache position. With k_norm_weight it is first RMS-normalised
+        like goda's k_norm (mint/nn/attn.py:58)."""
+        t = k.shape[1]
+        if self.len_bound is not None:
+            if self.len_bound + t > self.max_seq_len:
+                raise ValueError(
+                    f"KVCache.append: {t} rows after up to {self.len_bound} cached exceed max_seq_len {self.max_seq_len}"
+                )
+            self.len_bound += t
         ops.kv_append(
             k,
             v,
@@ -67,8 +91,11 @@ class KVCache:
             rope_cos=rope_cos,
             rope_sin=rope_sin,
             rope_k=rope_cos is not None,
+            rope_k_offset=0 if start_pos is None else int(start_pos),
+            rope_pos_abs=start_pos is not None,
             k_norm_weight=k_norm_weight,
             norm_eps=norm_eps,
+            status=self.status,
         )
 
     def update(self, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
@@ -78,22 +105,50 @@ class KVCache:
         if start_pos < 0 or start_pos + seq_len > self.max_seq_len:
             raise ValueError(f"KVCache.update: rows [{start_pos}, {start_pos + seq_len}) exceed max_seq_len {self.max_seq_len}")
         self.cache_seqlens[:batch_size].fill_(start_pos)
+        bound = self.len_bound
+        self.len_bound = None  # the append below is checked by the explicit range above
         self.append(k, v)
+        self.len_bound = None if bound is None else max(bound, start_pos + seq_len)
         end_pos = start_pos + seq_len
         return self.k_cache[:batch_size, :end_pos], self.v_cache[:batch_size, :end_pos]
 
+    def set_seqlens(self, lengths) -> None:
+        """Set cache_seqlens[:len(lengths)] (host values) and the host bound."""
+        lengths = torch.as_tensor(lengths, dtype=torch.int32)
+        if lengths.numel() and (int(lengths.min()) < 0 or int(lengths.max()) > self.max_seq_len):
+            raise ValueError(f"KVCache.set_seqlens: lengths must lie in [0, {self.max_seq_len}]")
+        self.cache_seqlens[: lengths.numel()] = lengths.to(self.cache_seqlens.device)
+        if self.len_bound is not None:
+            self.len_bound = max(self.len_bound, int(lengths.max()) if lengths.numel() else 0)
+
+    def check(self) -> None:
+        """Raise if an append ran past max_seq_len (reads the device status)."""
+        if int(self.status.item()) != 0:
+            raise RuntimeError(f"KVCache: an append ran past max_seq_len {self.max_seq_len}; rows past it were dropped")
+
     def get(self) -> tuple[torch.Tensor, torch.Tensor]:
         """mint/kvcache/base.py:52-54 (reads the length of sequence 0 on the host)."""
+        self.check()
         pos = int(self.cache_seqlens[0].item())
         return self.k_cache[:, :pos], self.v_cache[:, :pos]
 
+    def cache_tensors(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """The raw tensors for this package's own kernels (keeps len_bound)."""
+        return self.k_cache, self.v_cache, self.cache_seqlens
+
     def get_cache_tensors(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        # The caller may write the lengths: the host bound is no longer known.
+        self.len_bound = None
         return self.k_cache, self.v_cache, self.cache_seqlens
 
     def reset(self) -> None:
         self.cache_seqlens.zero_()
+        self.status.zero_()
+        self.len_bound = 0
 
     def clear(self) -> None:
         self.k_cache.zero_()
         self.v_cache.zero_()
         self.cache_seqlens.zero_()
+        self.status.zero_()
+        self.len_bound = 0

@@ -17,14 +17,19 @@ Without a KV cache the attention is differentiable: under autograd the
 backward runs on the HIP backward kernels (goda's training path,
 pretrain.py / sfttrain.py). The KV-cache path is inference only.
 
+`base_attn_mask` (a boolean mask broadcastable to [B, Hq, Lq, Lk], composed
+with the causal, window and doc masks as mint/nn/flashattn.py:236-255 does) is
+bit-packed and applied inside the forward and backward kernels. A right
+window is ignored, as the reference's SDPA path ignores it
+(mint/nn/flashattn.py:251-253).
+
 Extra keyword arguments fuse the positional encoding into the kernels:
 `rope=(cos, sin)` fp32 tables with `start_pos` (q and k are then passed
 UNROTATED), or `alibi_slopes` [Hq]; `qk_norm=(q_scale, k_scale, eps)` fuses
 goda's QK-RMSNorm (mint/nn/norm.py:17-27, weight 1 + scale, before RoPE) into
 the kernels' q/k loads when no gradient is needed (with autograd active it is
 applied as ordinary differentiable torch ops instead). There is no SDPA or
-CPU fallback: unsupported inputs (an arbitrary `base_attn_mask`, a right
-window) raise.
+CPU fallback.
 """
 
 from __future__ import annotations
@@ -68,35 +73,33 @@ class FlashAttention(nn.Module):
         base_attn_mask: torch.Tensor = None,
         doc_ids: torch.Tensor = None,
         rope: tuple[torch.Tensor, torch.Tensor] | None = None,
-        start_pos: int = 0,
+        start_pos: int | None = None,
         alibi_slopes: torch.Tensor | None = None,
         qk_norm: tuple[torch.Tensor, torch.Tensor, float] | None = None,
     ) -> torch.Tensor:
-        if base_attn_mask is not None:
-            raise NotImplementedError(
-                "goda_amd FlashAttention: an arbitrary base_attn_mask is not supported by the HIP kernels "
-                "(causal, left windows, doc_ids packing and ALiBi are)"
-            )
-        if window_size[1] != -1:
-            raise NotImplementedError("goda_amd FlashAttention: only left windows (window_size[1] == -1)")
+        # Only the left window is used: the reference's SDPA path reads
+        # window_size[0] alone (mint/nn/flashattn.py:251-253, 258-264).
+        window_left = window_size[0] if window_size[0] >= 0 else -1
         if qk_norm is not None and (doc_ids is not None or _needs_grad(q, k, *qk_norm[:2])):
             # Differentiable (or pre-rotation for doc_ids packing): plain torch.
             q, k = rms_norm(q, qk_norm[0], qk_norm[2]), rms_norm(k, qk_norm[1], qk_norm[2])
             qk_norm = None
         if kv_cache is None:
-            return self._attention(q, k, v, causal=causal, window_left=window_size[0], doc_ids=doc_ids,
-                                   rope=rope, start_pos=start_pos, alibi_slopes=alibi_slopes, qk_norm=qk_norm)
+            return self._attention(q, k, v, causal=causal, window_left=window_left, doc_ids=doc_ids,
+                                   base_attn_mask=base_attn_mask, rope=rope, start_pos=start_pos or 0,
+                                   alibi_slopes=alibi_slopes, qk_norm=qk_norm)
         if doc_ids is not None:
             raise NotImplementedError("goda_amd FlashAttention: doc_ids with a KV cache")
-        return self._attention_with_kvcache(q, k, v, kv_cache, causal=causal, window_left=window_size[0],
-                                            rope=rope, alibi_slopes=alibi_slopes, qk_norm=qk_norm)
+        return self._attention_with_kvcache(q, k, v, kv_cache, causal=causal, window_left=window_left,
+                                            base_attn_mask=base_attn_mask, rope=rope, start_pos=start_pos,
+                                            alibi_slopes=alibi_slopes, qk_norm=qk_norm)
 
     # mint/nn/flashattn.py:87-172
-    def _attention(self, q, k, v, *, causal, window_left, doc_ids, rope, start_pos, alibi_slopes, qk_norm):
+    def _attention(self, q, k, v, *, causal, window_left, doc_ids, base_attn_mask, rope, start_pos, alibi_slopes,
+                   qk_norm):
         b, t, hq, d = q.shape
         hkv = k.shape[2]
-        window_left = window_left if window_left >= 0 else -1
-        if doc_ids is not None:
+        if doc_ids is not None and base_attn_mask is None:
             if rope is not None:
                 # Positions are row positions, not document positions: rotate
                 # in place on the GPU before packing (RoPE is applied before
@@ -120,29 +123,49 @@ class FlashAttention(nn.Module):
         if rope is not None:
             kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True, rope_k=True,
                       rope_q_offset=start_pos, rope_k_offset=start_pos)
+        mask = base_attn_mask
+        if doc_ids is not None:
+            # Both masks: their conjunction, as the reference builds it
+            # (mint/nn/flashattn.py:238-243), on the dense kernel.
+            docs = doc_ids[:, None, :, None] == doc_ids[:, None, None, :]
+            mask = docs & mask.to(torch.bool)
+        if mask is not None:
+            kw["attn_mask"] = mask
         return autograd.attention_prefill(q, k, v, causal=causal, window_left=window_left,
                                           alibi_slopes=alibi_slopes, **kw)
 
     # mint/nn/flashattn.py:174-219
-    def _attention_with_kvcache(self, q, k, v, kv_cache: KVCache, *, causal, window_left, rope, alibi_slopes, qk_norm):
+    def _attention_with_kvcache(self, q, k, v, kv_cache: KVCache, *, causal, window_left, base_attn_mask, rope,
+                                start_pos, alibi_slopes, qk_norm):
+        """Append k/v at each sequence's cache length, then attend over the
+        visible cache. With fused RoPE and an integer `start_pos` (what goda's
+        attention layer passes), q and the new k rotate at start_pos + t, as
+        goda's RoPE(q, k, start_pos) does (mint/nn/pos.py:100-112); with
+        start_pos None they rotate at their cache positions."""
         b, tq = q.shape[0], q.shape[1]
-        window_left = window_left if window_left >= 0 else -1
-        kv_cache.append(k, v, **({} if rope is None else dict(rope_cos=rope[0], rope_sin=rope[1])),
+        rope_kw = {}
+        if rope is not None:
+            rope_kw = dict(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
+            if start_pos is not None:
+                rope_kw.update(rope_q_offset=int(start_pos), rope_pos_abs=True)
+        kv_cache.append(k, v, **({} if rope is None else dict(rope_cos=rope[0], rope_sin=rope[1],
+                                                              start_pos=start_pos)),
                         **_norm_kwargs(qk_norm, q=False, k=True))
-        k_cache, v_cache, seqlens = kv_cache.get_cache_tensors()
+        k_cache, v_cache, seqlens = kv_cache.cache_tensors()
         used = seqlens[:b]
-        if tq == 1:
-            kw = _norm_kwargs(qk_norm, q=True, k=False)
-            if rope is not None:
-                kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
+        kw = _norm_kwargs(qk_norm, q=True, k=False)
+        kw.update(rope_kw)
+        if tq == 1 and base_attn_mask is None:
             # One new token: the bottom-right causal mask admits every cached
             # key, so causal and non-causal coincide (mint/nn/flashattn.py:245-264).
             return ops.attention_decode(q, k_cache, v_cache, used, window_left=window_left,
                                         alibi_slopes=alibi_slopes, **kw)
-        kw = _norm_kwargs(qk_norm, q=True, k=False)
-        if rope is not None:
-            kw.update(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
-        return ops.attention_prefill(q, k_cache[:b], v_cache[:b], causal=causal, window_left=window_left,
+        # Chunked prefill over the cache: the launch covers the keys the cache
+        # can hold now (its host-side length bound), not max_seq_len.
+        lk = kv_cache.max_seq_len if kv_cache.len_bound is None else max(1, kv_cache.len_bound)
+        if base_attn_mask is not None:
+            kw["attn_mask"] = base_attn_mask
+        return ops.attention_prefill(q, k_cache[:b, :lk], v_cache[:b, :lk], causal=causal, window_left=window_left,
                                      alibi_slopes=alibi_slopes, seqused_k=used, **kw)
 
 

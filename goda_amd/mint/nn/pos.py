@@ -15,13 +15,21 @@ import torch
 from torch import nn
 
 
+def rope_tables(seq_len: int, head_dim: int, base: float, scale_factor: float = 1.0):
+    """fp32 cos/sin [seq_len, head_dim/2] of goda's RoPE buffers
+    (mint/nn/pos.py:71-88): inv_freq_i = base^(-2i/D), theta = t * inv_freq,
+    with t = position / scale_factor for LinearScaledRoPE (:127-148)."""
+    channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
+    inv_freq = 1.0 / (base ** (channel_range / head_dim))
+    t = torch.arange(seq_len, dtype=torch.float32)
+    if scale_factor != 1.0:
+        t = t / scale_factor
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos(), freqs.sin()
+
+
 class PosEmbeddings(nn.Module):
     """Base of the fusable encodings (mint/nn/pos.py:8-15)."""
-
-    def kernel_args(self) -> dict:
-        """Keyword arguments for goda_amd.ops / FlashAttention that fuse this
-        encoding into the attention kernel."""
-        raise NotImplementedError
 
 
 class RoPE(PosEmbeddings):
@@ -34,23 +42,14 @@ class RoPE(PosEmbeddings):
     def __init__(self, seq_len: int, head_dim: int, rope_base_theta: int = 100000, dtype: torch.dtype = torch.float32) -> None:
         super().__init__()
         self.head_dim = head_dim
-        cos, sin = self._tables(seq_len, head_dim, float(rope_base_theta))
+        cos, sin = rope_tables(seq_len, head_dim, float(rope_base_theta), self._scale_factor())
         self.register_buffer("cos", cos, persistent=False)
         self.register_buffer("sin", sin, persistent=False)
         self.cos: torch.Tensor
         self.sin: torch.Tensor
 
-    def _positions(self, seq_len: int) -> torch.Tensor:
-        return torch.arange(seq_len, dtype=torch.float32)
-
-    def _tables(self, seq_len: int, head_dim: int, base: float):
-        channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
-        inv_freq = 1.0 / (base ** (channel_range / head_dim))
-        freqs = torch.outer(self._positions(seq_len), inv_freq)
-        return freqs.cos(), freqs.sin()  # [seq_len, head_dim/2] fp32
-
-    def kernel_args(self) -> dict:
-        return {"rope_cos": self.cos, "rope_sin": self.sin}
+    def _scale_factor(self) -> float:
+        return 1.0
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, start_pos: int = 0):
         t = q.shape[1]
@@ -79,8 +78,8 @@ class LinearScaledRoPE(RoPE):
         self.scale_factor = scale_factor
         super().__init__(seq_len, head_dim, rope_base_theta, dtype)
 
-    def _positions(self, seq_len: int) -> torch.Tensor:
-        return torch.arange(seq_len, dtype=torch.float32) / self.scale_factor
+    def _scale_factor(self) -> float:
+        return float(self.scale_factor)
 
 
 def alibi_slopes(n_heads: int) -> list[float]:
@@ -108,9 +107,6 @@ class ALiBiPositionalBias(PosEmbeddings):
         self.n_heads = n_heads
         self.register_buffer("slopes", torch.tensor(alibi_slopes(n_heads), dtype=torch.float32), persistent=False)
         self.slopes: torch.Tensor
-
-    def kernel_args(self) -> dict:
-        return {"alibi_slopes": self.slopes}
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, start_pos: int = 0):
         seq_len_q = q.shape[1]

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from typing import NamedTuple
 
 import torch
 
@@ -62,6 +63,61 @@ def _f32_vec(name: str, t: torch.Tensor | None, n: int, device: torch.device) ->
     if t.numel() != n:
         raise ValueError(f"goda_amd: {name} must have {n} elements")
     return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+class PackedMask(NamedTuple):
+    """A boolean attention mask bit-packed along the key axis for the C-ABI
+    (goda_prefill_args.mask_bits): int32 words [Bm, Hm, Lqm, W] with
+    W = 2 * ceil(seqlen_k / 64); bit j % 32 of word j // 32 is key j. Strides
+    are in words, 0 where the mask broadcasts (Bm, Hm or Lqm of 1)."""
+
+    bits: torch.Tensor
+    stride_b: int
+    stride_h: int
+    stride_q: int
+    seqlen_k: int
+
+
+def pack_mask(mask: torch.Tensor, batch: int, heads_q: int, seqlen_q: int, seqlen_k: int, device) -> PackedMask:
+    """Bit-pack goda's boolean `base_attn_mask` (mint/nn/flashattn.py:242-243),
+    broadcastable to the attention-weight shape [B, Hq, Lq, Lk]. A key
+    dimension shorter than seqlen_k (a KV-cache launch sized past the keys
+    the mask names) hides the remaining keys; a key dimension of 1
+    broadcasts over every key."""
+    if isinstance(mask, PackedMask):
+        if mask.seqlen_k < seqlen_k:
+            raise ValueError(f"goda_amd: packed mask covers {mask.seqlen_k} keys, the launch has {seqlen_k}")
+        return mask
+    if mask.dtype != torch.bool:
+        raise ValueError(f"goda_amd: base_attn_mask must be boolean (got {mask.dtype})")
+    m = mask
+    while m.dim() < 4:
+        m = m.unsqueeze(0)
+    if m.dim() != 4:
+        raise ValueError(f"goda_amd: base_attn_mask {tuple(mask.shape)} has more than 4 dimensions")
+    for size, full, name in zip(m.shape[:3], (batch, heads_q, seqlen_q), ("batch", "heads", "query")):
+        if size not in (1, full):
+            raise ValueError(f"goda_amd: base_attn_mask {tuple(mask.shape)} does not broadcast over {name} size {full}")
+    if m.shape[3] != 1 and m.shape[3] > seqlen_k:
+        raise ValueError(f"goda_amd: base_attn_mask has {m.shape[3]} keys, more than the {seqlen_k} attended")
+    m = m.to(device)
+    bm, hm, qm, lk = m.shape
+    if lk == 1:
+        m = m.expand(bm, hm, qm, seqlen_k)
+        lk = seqlen_k
+    words = 2 * ((seqlen_k + 63) // 64)
+    u8 = torch.zeros(bm, hm, qm, words * 32, dtype=torch.uint8, device=device)
+    u8[..., :lk] = m
+    weights = torch.tensor([1, 2, 4, 8, 16, 32, 64, 128], dtype=torch.uint8, device=device)
+    by = (u8.view(bm, hm, qm, words * 4, 8) * weights).sum(-1, dtype=torch.uint8)
+    bits = by.contiguous().view(torch.int32)  # little-endian: byte k holds keys 8k .. 8k+7
+    return PackedMask(
+        bits,
+        bits.stride(0) if bm > 1 else 0,
+        bits.stride(1) if hm > 1 else 0,
+        bits.stride(2) if qm > 1 else 0,
+        seqlen_k,
+    )
 
 
 def _rope_tables(cos: torch.Tensor | None, sin: torch.Tensor | None, head_dim: int, device):
@@ -156,9 +212,11 @@ def _prefill_args(
     rope_k: bool = False,
     rope_q_offset: int = 0,
     rope_k_offset: int = 0,
+    rope_pos_abs: bool = False,
     q_norm_weight: torch.Tensor | None = None,
     k_norm_weight: torch.Tensor | None = None,
     norm_eps: float = 1e-6,
+    attn_mask: torch.Tensor | PackedMask | None = None,
     cu_seqlens_q: torch.Tensor | None = None,
     cu_seqlens_k: torch.Tensor | None = None,
     max_seqlen_q: int | None = None,
@@ -170,7 +228,11 @@ def _prefill_args(
 ):
     """Validated `PrefillArgs` for q, k, v and the options, with `o` (`out`
     or a new tensor) and `lse` (`lse_in`, a new tensor if `return_lse`, or
-    None). Returns (args, tensors to keep alive, o, lse); no workspace."""
+    None). Returns (args, tensors to keep alive, o, lse); no workspace.
+    `attn_mask` is a boolean mask broadcastable to [B, Hq, Lq, Lk] (or a
+    `PackedMask`), composed with causal / window like goda's base_attn_mask;
+    `rope_pos_abs` rotates query row i at rope_q_offset + i instead of
+    rope_q_offset + (Lk - Lq) + i."""
     for name, t in (("q", q), ("k", k), ("v", v)):
         _require_gpu(name, t)
         _require_last_contig(name, t)
@@ -262,11 +324,19 @@ def _prefill_args(
     a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
     a.rope_q, a.rope_k = int(bool(rope_q)), int(bool(rope_k))
     a.rope_q_offset, a.rope_k_offset = int(rope_q_offset), int(rope_k_offset)
+    a.rope_pos_abs = int(bool(rope_pos_abs))
     qn = _f32_vec("q_norm_weight", q_norm_weight, d, dev)
     kn = _f32_vec("k_norm_weight", k_norm_weight, d, dev)
     a.q_norm_weight, a.k_norm_weight, a.norm_eps = _ptr(qn), _ptr(kn), float(norm_eps)
+    pm = None
+    if attn_mask is not None:
+        if varlen:
+            raise ValueError("goda_amd: attn_mask needs dense q/k/v (not cu_seqlens)")
+        pm = pack_mask(attn_mask, batch, hq, tq, tk, dev)
+        a.mask_bits = pm.bits.data_ptr()
+        a.mask_stride_b, a.mask_stride_h, a.mask_stride_q = pm.stride_b, pm.stride_h, pm.stride_q
 
-    keep = (q, k, v, o, lse, slopes, cos, sin, cu_q, cu_k, used, qn, kn)
+    keep = (q, k, v, o, lse, slopes, cos, sin, cu_q, cu_k, used, qn, kn, pm)
     return a, keep, o, lse
 
 
@@ -348,6 +418,7 @@ def plan_decode(
     rope_sin: torch.Tensor | None = None,
     rope_q: bool = False,
     rope_q_offset: int = 0,
+    rope_pos_abs: bool = False,
     q_norm_weight: torch.Tensor | None = None,
     norm_eps: float = 1e-6,
     split_size: int = 0,
@@ -362,7 +433,9 @@ def plan_decode(
     q: [B, Hq, D] (or [B, 1, Hq, D]); caches [B, Lmax, Hkv, D] when
     cache_layout == "bthd" (goda's KVCache, mint/kvcache/base.py:22-31) or
     [B, Hkv, Lmax, D] when "bhtd"; cache_seqlens int32 [B] = valid keys
-    (the new token included). The query sits at position cache_seqlens[b]-1.
+    (the new token included). The query sits at position cache_seqlens[b]-1
+    and is rotated there (+ rope_q_offset), or at rope_q_offset itself with
+    `rope_pos_abs` (a caller-given position, goda's start_pos).
     With `noalloc` the launch goes through `goda_attn_decode_noalloc`, whose
     split-K partials live in the library's fixed device-resident array (no
     workspace; calls overlapping on one GPU race).
@@ -397,7 +470,13 @@ def plan_decode(
         raise ValueError(f"goda_amd: heads_q {hq} is not a multiple of heads_kv {hkv}")
     dev = q.device
     seqlens = _i32_vec("cache_seqlens", cache_seqlens[:b] if cache_seqlens.numel() > b else cache_seqlens, b, dev)
-    o = torch.empty_like(q) if out is None else out
+    if out is None:
+        o = torch.empty_like(q)
+    else:
+        if out.shape != q.shape or out.dtype != q.dtype or out.device != dev:
+            raise ValueError(f"goda_amd: out must be {tuple(q.shape)} {q.dtype} on {dev}")
+        _require_last_contig("out", out)
+        o = out
     lse = torch.empty((b, hq), dtype=torch.float32, device=dev) if return_lse else None
     slopes = _f32_vec("alibi_slopes", alibi_slopes, hq, dev)
     cos, sin, rope_len = _rope_tables(rope_cos, rope_sin, d, dev)
@@ -423,6 +502,7 @@ def plan_decode(
     a.alibi_slopes = _ptr(slopes)
     a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
     a.rope_q, a.rope_q_offset = int(bool(rope_q)), int(rope_q_offset)
+    a.rope_pos_abs = int(bool(rope_pos_abs))
     qn = _f32_vec("q_norm_weight", q_norm_weight, d, dev)
     a.q_norm_weight, a.norm_eps = _ptr(qn), float(norm_eps)
 
@@ -451,14 +531,20 @@ def kv_append(
     rope_sin: torch.Tensor | None = None,
     rope_k: bool = False,
     rope_k_offset: int = 0,
+    rope_pos_abs: bool = False,
     k_norm_weight: torch.Tensor | None = None,
     norm_eps: float = 1e-6,
+    status: torch.Tensor | None = None,
 ) -> None:
     """Write k_new/v_new [B, Tn, Hkv, D] into caches [Bmax, Lmax, Hkv, D] at
     each sequence's own position cache_seqlens[b], then advance the lengths —
     all on the device, with no host read of the lengths. k rows are
     optionally RMS-normalised (goda's RMSNorm with weight 1 + k_norm_weight)
-    and then rotated before they are stored."""
+    and then rotated before they are stored: row t at its cache position
+    (+ rope_k_offset), or at rope_k_offset + t with `rope_pos_abs`.
+    A sequence whose rows would pass Lmax keeps the rows that fit, its length
+    stops at Lmax, and 1 is stored into `status` (an int32 GPU tensor the
+    caller clears and checks) when given."""
     for name, t in (("k_new", k_new), ("v_new", v_new), ("k_cache", k_cache), ("v_cache", v_cache)):
         _require_gpu(name, t)
         _require_last_contig(name, t)
@@ -467,6 +553,10 @@ def kv_append(
     b, tn, hkv, d = k_new.shape
     if v_new.shape != k_new.shape or k_cache.shape[2:] != (hkv, d) or k_cache.shape != v_cache.shape:
         raise ValueError("goda_amd: kv_append shapes do not match")
+    if k_cache.shape[0] < b:
+        raise ValueError(f"goda_amd: kv_append of {b} sequences into a cache of {k_cache.shape[0]}")
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1 or status.device != k_new.device):
+        raise ValueError("goda_amd: status must be an int32 tensor on the cache's device")
     if cache_seqlens.dtype != torch.int32 or cache_seqlens.numel() < b or not cache_seqlens.is_contiguous():
         raise ValueError("goda_amd: cache_seqlens must be a contiguous int32 vector")
     dev = k_new.device
@@ -486,6 +576,8 @@ def kv_append(
     a.cache_seqlens = cache_seqlens.data_ptr()
     a.rope_cos, a.rope_sin, a.rope_len = _ptr(cos), _ptr(sin), rope_len
     a.rope_k, a.rope_k_offset = int(bool(rope_k)), int(rope_k_offset)
+    a.rope_pos_abs = int(bool(rope_pos_abs))
+    a.status = _ptr(status)
     kn = _f32_vec("k_norm_weight", k_norm_weight, d, dev)
     a.k_norm_weight, a.norm_eps = _ptr(kn), float(norm_eps)
     _lib.check(_lib.load().goda_attn_kv_append(ctypes.byref(a), _stream()))

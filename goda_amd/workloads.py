@@ -22,6 +22,8 @@ from dataclasses import dataclass, field
 
 import torch
 
+from .mint.nn.pos import alibi_slopes, rope_tables  # noqa: F401  (re-exported for the tests and bench)
+
 BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 4096 flop/clk x 2.4 GHz)
 FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBPS = 8000.0
@@ -91,31 +93,6 @@ def _randn(shape, std, dtype, device, gen):
     return (torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
 
 
-def rope_tables(seq_len: int, head_dim: int, base: float, device="cpu", scale_factor: float = 1.0):
-    """fp32 cos/sin [seq_len, head_dim/2] computed as goda's RoPE buffers
-    (mint/nn/pos.py:71-88; LinearScaledRoPE divides t, :127-148)."""
-    channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
-    inv_freq = 1.0 / (base ** (channel_range / head_dim))
-    t = torch.arange(seq_len, dtype=torch.float32)
-    if scale_factor != 1.0:
-        t = t / scale_factor
-    freqs = torch.outer(t, inv_freq)
-    return freqs.cos().to(device), freqs.sin().to(device)
-
-
-def alibi_slopes(n_heads: int) -> list[float]:
-    """goda's ALiBi slopes (mint/nn/pos.py:171-184)."""
-
-    def pow2(n: int) -> list[float]:
-        start = 2 ** (-(2 ** -(math.log2(n) - 3)))
-        return [start * (start**i) for i in range(n)]
-
-    if math.log2(n_heads).is_integer():
-        return pow2(n_heads)
-    closest = 2 ** math.floor(math.log2(n_heads))
-    return pow2(closest) + alibi_slopes(2 * closest)[0::2][: n_heads - closest]
-
-
 def seq_lengths(lo: int, hi: int, n: int, seed: int) -> torch.Tensor:
     g = torch.Generator()
     g.manual_seed(seed)
@@ -144,7 +121,7 @@ def prefill_inputs(w: Prefill, device="cuda") -> dict:
     out["k"] = _randn(shape_k, w.std, w.dtype, device, gen)
     out["v"] = _randn(shape_k, w.std, w.dtype, device, gen)
     if w.rope_base is not None:
-        out["rope_cos"], out["rope_sin"] = rope_tables(w.seqlen, w.head_dim, w.rope_base, device)
+        out["rope_cos"], out["rope_sin"] = (t.to(device) for t in rope_tables(w.seqlen, w.head_dim, w.rope_base))
     if w.alibi:
         out["alibi_slopes"] = torch.tensor(alibi_slopes(w.heads_q), dtype=torch.float32, device=device)
     return out
@@ -166,7 +143,7 @@ def decode_inputs(w: Decode, device="cuda") -> dict:
         "cache_seqlens": lens.to(device),
     }
     if w.rope_base is not None:
-        out["rope_cos"], out["rope_sin"] = rope_tables(w.max_seqlen, w.head_dim, w.rope_base, device)
+        out["rope_cos"], out["rope_sin"] = (t.to(device) for t in rope_tables(w.max_seqlen, w.head_dim, w.rope_base))
     return out
 
 

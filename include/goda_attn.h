@@ -28,8 +28,12 @@
  *     (mint/nn/pos.py:186-207);
  *   - RoPE is the half-split rotation of mint/nn/pos.py:90-98 with caller
  *     supplied fp32 cos/sin tables [rope_len, head_dim/2]; query row i is
- *     rotated at position rope_q_offset + (Lk - Lq) + i, key row j at
+ *     rotated at position rope_q_offset + (Lk - Lq) + i (rope_pos_abs = 0)
+ *     or rope_q_offset + i (rope_pos_abs = 1), key row j at
  *     rope_k_offset + j;
+ *   - an optional boolean mask (goda's base_attn_mask,
+ *     mint/nn/flashattn.py:242-243) further hides keys: bit-packed, see
+ *     goda_prefill_args.mask_bits;
  *   - the optional fused QK-RMSNorm is goda's RMSNorm (mint/nn/norm.py:17-27)
  *     as applied to q and k before RoPE (mint/nn/attn.py:57-60): a head row
  *     x becomes x * rsqrt(mean(x^2) + norm_eps) * (1 + w) in fp32, with a
@@ -51,7 +55,7 @@
 extern "C" {
 #endif
 
-#define GODA_ATTN_ABI_VERSION 3
+#define GODA_ATTN_ABI_VERSION 4
 
 /* element types */
 #define GODA_DTYPE_F32 0
@@ -105,11 +109,28 @@ typedef struct goda_prefill_args {
   int32_t rope_q_offset;
   int32_t rope_k_offset;
   float norm_eps;              /* epsilon of the fused RMSNorm (goda: 1e-6) */
+  int32_t rope_pos_abs;        /* 1: query row i rotates at rope_q_offset + i
+                                  (a caller-given start position, as goda's
+                                  RoPE(q, k, start_pos), mint/nn/pos.py:100-112);
+                                  0: at rope_q_offset + (Lk - Lq) + i */
 
   /* Fused QK-RMSNorm weights, fp32 [head_dim] each, or NULL (no norm on
    * that side). Forward only: goda_attn_prefill_bwd rejects them. */
   const float* q_norm_weight;
   const float* k_norm_weight;
+
+  /* Optional boolean mask composed with causal / window / ALiBi, goda's
+   * base_attn_mask (mint/nn/flashattn.py:242-243, broadcastable to
+   * [B, Hq, Lq, Lk]): key j is visible to query row i (0-based within its
+   * sequence) of query head h in sequence b only if bit j % 32 of word
+   *   mask_bits[b*mask_stride_b + h*mask_stride_h + i*mask_stride_q + j/32]
+   * is 1. Strides are in 32-bit words (0 broadcasts that dimension) and must
+   * be even, the pointer 8-byte aligned, and every row must hold
+   * 2*ceil(seqlen_k/64) readable words (bits past the keys are ignored).
+   * Dense launches only (cu_seqlens NULL). NULL: no mask. A row that sees no
+   * key produces o = 0 and lse = -inf. */
+  const uint32_t* mask_bits;
+  int64_t mask_stride_b, mask_stride_h, mask_stride_q;
 
   void* workspace;             /* size from goda_attn_prefill_workspace_size */
   int64_t workspace_bytes;
@@ -132,7 +153,8 @@ typedef struct goda_decode_args {
   int32_t split_size;   /* keys per work range (multiple of 64); 0 = the visible
                            keys of all sequences spread evenly over the GPU */
   float softmax_scale;
-  int32_t reserved0;
+  int32_t rope_pos_abs; /* 1: q rotates at rope_q_offset (a caller-given
+                           position); 0: at cache_seqlens[b] - 1 + rope_q_offset */
 
   const void* q;        /* [batch, heads_q, head_dim]: one new token per sequence */
   int64_t q_stride_b, q_stride_h;
@@ -147,7 +169,7 @@ typedef struct goda_decode_args {
   int64_t lse_stride_b;
 
   const float* alibi_slopes; /* [heads_q] or NULL */
-  const float* rope_cos;     /* rotate q at position cache_seqlens[b]-1+rope_q_offset */
+  const float* rope_cos;     /* rotate q (position: see rope_pos_abs) */
   const float* rope_sin;
   int32_t rope_len;
   int32_t rope_q;
@@ -179,14 +201,23 @@ typedef struct goda_kv_append_args {
   int64_t k_stride_b, k_stride_t, k_stride_h;
   void* v_cache;
   int64_t v_stride_b, v_stride_t, v_stride_h;
-  int32_t* cache_seqlens; /* [batch]: in = write position, out = position + seqlen_new */
-  const float* rope_cos;  /* rotate new k rows at their cache position + rope_k_offset */
+  int32_t* cache_seqlens; /* [batch]: in = write position, out = position + seqlen_new,
+                             clamped to max_seqlen */
+  const float* rope_cos;  /* rotate new k row t at (cache position + rope_k_offset), or
+                             at rope_k_offset + t with rope_pos_abs */
   const float* rope_sin;
   int32_t rope_len;
   int32_t rope_k;
   int32_t rope_k_offset;
   float norm_eps;
   const float* k_norm_weight; /* fused RMSNorm of new k rows before RoPE, fp32 [head_dim], or NULL */
+  int32_t rope_pos_abs;
+  int32_t reserved0;
+  /* Overflow report, or NULL: a sequence whose rows would pass max_seqlen
+   * keeps only the rows that fit, its length stops at max_seqlen, and the
+   * launch stores 1 here (never 0: the caller clears it). goda's
+   * KVCache.update fails on the same input (mint/kvcache/base.py:40-43). */
+  int32_t* status;
 } goda_kv_append_args;
 
 /* Gradients for goda_attn_prefill_bwd. Every tensor uses the (b, t, h)

@@ -165,13 +165,16 @@ def attention(
     window_size: tuple[int, int] = (-1, -1),
     doc_ids: torch.Tensor | None = None,
     alibi_slopes: torch.Tensor | None = None,
+    base_attn_mask: torch.Tensor | None = None,
     scale: float | None = None,
     dtype=torch.float32,
 ) -> torch.Tensor:
     """FlashAttention._attention's SDPA branch (mint/nn/flashattn.py:156-172).
 
     q [B, Tq, Hq, D], k/v [B, Tk, Hkv, D] -> [B, Tq, Hq, D], computed in
-    `dtype` on the CPU.
+    `dtype` on the CPU. `base_attn_mask` is goda's boolean mask, broadcastable
+    to [B, Hq, Tq, Tk] (mint/nn/flashattn.py:242-243). A row that sees no key
+    comes out as 0 (this torch's SDPA zeroes fully masked rows).
     """
     qs = q.to("cpu", dtype).transpose(1, 2)
     ks = k.to("cpu", dtype).transpose(1, 2)
@@ -179,7 +182,10 @@ def attention(
     alibi = None
     if alibi_slopes is not None:
         alibi = alibi_bias(alibi_slopes.to("cpu", dtype), qs.size(2), ks.size(2), dtype)
-    out = sdpa_attention(qs, ks, vs, causal=causal, window_size=window_size, doc_ids=doc_ids, alibi=alibi, scale=scale)
+    if base_attn_mask is not None:
+        base_attn_mask = base_attn_mask.to("cpu")
+    out = sdpa_attention(qs, ks, vs, causal=causal, window_size=window_size, doc_ids=doc_ids, alibi=alibi,
+                         base_attn_mask=base_attn_mask, scale=scale)
     return out.transpose(1, 2)
 
 
@@ -195,12 +201,14 @@ def attention_rows(
     scale: float | None = None,
     dtype=torch.float32,
     lk: torch.Tensor | None = None,
+    base_attn_mask: torch.Tensor | None = None,
 ):
     """Same semantics as `attention` for a subset of query rows, one batch
     entry at a time, without materialising [Tq, Tk] for all rows: returns
     (o [B, len(rows), Hq, D], lse [B, Hq, len(rows)]). Used to check full-size
     configurations on sampled rows. `lk` optionally gives per-sequence key
-    counts (keys >= lk[b] are absent).
+    counts (keys >= lk[b] are absent); `base_attn_mask` is goda's boolean
+    mask broadcastable to [B, Hq, Tq, Tk].
     """
     b_, tq, hq, d = q.shape
     tk, hkv = k.shape[1], k.shape[2]
@@ -226,7 +234,14 @@ def attention_rows(
         if alibi_slopes is not None:
             rel = (j[None, :] - iabs[:, None]).to(dtype)
             s = s + alibi_slopes.to("cpu", dtype)[:, None, None] * rel[None]
-        s = s.masked_fill(~vis[None], float("-inf"))
+        visb = vis[None]
+        if base_attn_mask is not None:
+            m = base_attn_mask.to("cpu")
+            while m.dim() < 4:
+                m = m.unsqueeze(0)
+            m = m.expand(b_, hq, tq, m.shape[-1] if m.shape[-1] != 1 else tk)
+            visb = visb & m[b][:, rows, :L]
+        s = s.masked_fill(~visb, float("-inf"))
         lse = torch.logsumexp(s, dim=-1)  # [Hq, R]
         p = torch.exp(s - lse[..., None])
         p = torch.nan_to_num(p, nan=0.0)
@@ -384,6 +399,7 @@ def attention_grads(
     window_size: tuple[int, int] = (-1, -1),
     doc_ids: torch.Tensor | None = None,
     alibi_slopes: torch.Tensor | None = None,
+    base_attn_mask: torch.Tensor | None = None,
     rope: tuple | None = None,
     scale: float | None = None,
     dtype=torch.float32,
@@ -398,7 +414,7 @@ def attention_grads(
     `rope` = (cos, sin, q_positions, k_positions) rotates q and k first
     (mint/nn/pos.py:90-112, applied before attention at mint/nn/attn.py:60),
     so dq/dk refer to the unrotated inputs. Every query row must see at least
-    one key (SDPA returns NaN for a row with none).
+    one key, or come out of `attention` as 0 (then its gradients are 0).
     """
     qs = q.to("cpu", dtype).detach().requires_grad_(True)
     ks = k.to("cpu", dtype).detach().requires_grad_(True)
@@ -410,7 +426,7 @@ def attention_grads(
         kr = apply_rope(ks, cos, sin, kpos)
     with torch.enable_grad():
         o = attention(qr, kr, vs, causal=causal, window_size=window_size, doc_ids=doc_ids,
-                      alibi_slopes=alibi_slopes, scale=scale, dtype=dtype)
+                      alibi_slopes=alibi_slopes, base_attn_mask=base_attn_mask, scale=scale, dtype=dtype)
         o.backward(d_o.to("cpu", dtype))
     return qs.grad, ks.grad, vs.grad
 
@@ -423,3 +439,63 @@ def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6) -> torch.T
     var = x_f.pow(2).mean(dim=-1, keepdim=True)
     out = x_f * torch.rsqrt(var + eps) * (1.0 + scale.to(x_f.dtype))
     return out.to(x.dtype)
+
+
+def attention_grads_chunked(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    d_o: torch.Tensor,
+    *,
+    causal: bool,
+    alibi_slopes: torch.Tensor | None = None,
+    scale: float | None = None,
+    rows: torch.Tensor | None = None,
+    chunk: int = 1024,
+    dtype=torch.float32,
+):
+    """Gradients of one sequence's attention for one KV head's query group,
+    computed over query-row chunks so that no [Tq, Tk] matrix of the whole
+    sequence is held: q / d_o [Tq, G, D] (the G query heads that share the KV
+    head), k / v [Tk, D]. Returns (dq [len(rows), G, D], dk [Tk, D],
+    dv [Tk, D]); dk / dv sum the G heads (the GQA reduction) and are complete
+    only when `rows` is every row (the default).
+
+    The FlashAttention-2 backward of kernels_/flash_attn_gqa/cuda.py:6-246
+    per chunk, with the chunk's own exact softmax: P = softmax(s), o = P v,
+    delta = rowsum(dO * o), dS = P * (dO v^T - delta), dq = scale dS k,
+    dk += scale dS^T q, dv += P^T dO. Causal alignment is bottom-right, ALiBi
+    adds slope_h * (j - i_abs). Inputs are already rotated (RoPE is the
+    caller's). Rows with no visible key contribute nothing.
+    """
+    tq, g, d = q.shape
+    tk = k.shape[0]
+    scale = scale if scale is not None else 1.0 / math.sqrt(d)
+    rows = torch.arange(tq) if rows is None else rows.to(torch.long)
+    qd, od = q.to("cpu", dtype), d_o.to("cpu", dtype)
+    kd, vd = k.to("cpu", dtype), v.to("cpu", dtype)
+    dq = torch.zeros(len(rows), g, d, dtype=dtype)
+    dk = torch.zeros(tk, d, dtype=dtype)
+    dv = torch.zeros(tk, d, dtype=dtype)
+    for c0 in range(0, len(rows), chunk):
+        r = rows[c0 : c0 + chunk]
+        iabs = (tk - tq) + r  # [R]
+        kmax = int(iabs.max()) + 1 if causal else tk  # keys any row of the chunk can see
+        kmax = max(0, min(kmax, tk))
+        kc, vc = kd[:kmax], vd[:kmax]
+        j = torch.arange(kmax)
+        s = torch.einsum("rgd,jd->grj", qd[r], kc) * scale  # [G, R, J]
+        if alibi_slopes is not None:
+            s = s + alibi_slopes.to("cpu", dtype)[:, None, None] * (j[None, :] - iabs[:, None]).to(dtype)[None]
+        if causal:
+            s = s.masked_fill((j[None, :] > iabs[:, None])[None], float("-inf"))
+        lse = torch.logsumexp(s, dim=-1, keepdim=True)
+        p = torch.nan_to_num(torch.exp(s - lse), nan=0.0)  # rows with no key: 0
+        o = torch.einsum("grj,jd->rgd", p, vc)
+        delta = (od[r] * o).sum(-1)  # [R, G]
+        dp = torch.einsum("rgd,jd->grj", od[r], vc)
+        ds = p * (dp - delta.T[:, :, None])
+        dq[c0 : c0 + chunk] = torch.einsum("grj,jd->rgd", ds, kc) * scale
+        dk[:kmax] += torch.einsum("grj,rgd->jd", ds, qd[r]) * scale
+        dv[:kmax] += torch.einsum("grj,rgd->jd", p, od[r])
+    return dq, dk, dv

@@ -23,13 +23,15 @@ def attention(
     window_left: int = -1,
     slopes: np.ndarray | None = None,
     doc_ids: np.ndarray | None = None,
+    mask: np.ndarray | None = None,
     scale: float | None = None,
 ):
     """q [B, Tq, Hq, D], k/v [B, Tk, Hkv, D] -> (o [B, Tq, Hq, D], lse [B, Hq, Tq]).
 
     Query row i of Tq sits at absolute position i_abs = Tk - Tq + i; key j is
     visible iff (not causal or j <= i_abs) and (window: i_abs - j <= W, with
-    causal or Tq == 1) and (doc ids equal). Bias slope_h * (j - i_abs).
+    causal or Tq == 1) and (doc ids equal) and (mask[b, h, i, j], a boolean
+    array broadcastable to [B, Hq, Tq, Tk]). Bias slope_h * (j - i_abs).
     A row with no visible key gives o = 0, lse = -inf.
     """
     q = q.astype(np.float64)
@@ -39,6 +41,8 @@ def attention(
     tk, hkv = k.shape[1], k.shape[2]
     group = hq // hkv
     scale = 1.0 / math.sqrt(d) if scale is None else scale
+    if mask is not None:
+        mask = np.broadcast_to(mask, (b_, hq, tq, tk))
     o = np.zeros((b_, tq, hq, d))
     lse = np.full((b_, hq, tq), -np.inf)
     for b in range(b_):
@@ -54,6 +58,8 @@ def attention(
                     if window_left >= 0 and (causal or tq == 1) and iabs - j > window_left:
                         continue
                     if doc_ids is not None and doc_ids[b, i] != doc_ids[b, j]:
+                        continue
+                    if mask is not None and not mask[b, h, i, j]:
                         continue
                     s = float(np.dot(q[b, i, h], k[b, j, hk])) * scale
                     if slopes is not None:
@@ -101,6 +107,7 @@ def attention_backward(
     window_left: int = -1,
     slopes: np.ndarray | None = None,
     doc_ids: np.ndarray | None = None,
+    mask: np.ndarray | None = None,
     scale: float | None = None,
     plant: str | None = None,
 ):
@@ -124,7 +131,10 @@ def attention_backward(
     tk, hkv = k.shape[1], k.shape[2]
     group = hq // hkv
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    o, lse = attention(q, k, v, causal=causal, window_left=window_left, slopes=slopes, doc_ids=doc_ids, scale=scale)
+    o, lse = attention(q, k, v, causal=causal, window_left=window_left, slopes=slopes, doc_ids=doc_ids, mask=mask,
+                       scale=scale)
+    if mask is not None:
+        mask = np.broadcast_to(mask, (b_, hq, tq, tk))
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)
     dv = np.zeros_like(v)
@@ -143,6 +153,8 @@ def attention_backward(
                     if window_left >= 0 and (causal or tq == 1) and iabs - j > window_left:
                         continue
                     if doc_ids is not None and doc_ids[b, i] != doc_ids[b, j]:
+                        continue
+                    if mask is not None and not mask[b, h, i, j]:
                         continue
                     s = float(np.dot(q[b, i, h], k[b, j, hk])) * scale
                     if slopes is not None:

@@ -2,10 +2,11 @@
 against the CPU oracle's gradients (torch autograd through the SDPA
 restatement, pinned by tests/test_oracle.py against finite differences).
 
-Tolerance: the north-star bounds (1e-4 fp32, 2e-2 bf16/fp16) applied to the
-gradient error normalised by max(1, max |reference gradient|), because
-gradient magnitudes grow with the number of rows and group heads that feed
-one key.
+Tolerance: the north-star absolute bounds (1e-4 fp32, 2e-2 bf16/fp16) on top of
+the gradient's own storage rounding at the largest reference value (2^-8 |x|
+in bf16, 2^-11 |x| in fp16, 2^-24 |x| in fp32): gradient magnitudes grow with
+the number of rows and group heads that feed one key, and a 16-bit output
+cannot hold x more closely than its rounding.
 """
 
 from __future__ import annotations
@@ -33,16 +34,24 @@ def _rand(shape, dtype, seed, std=0.5):
     return (torch.randn(shape, generator=g) * std).to(dtype)
 
 
-def grad_err(x: torch.Tensor, x_ref: torch.Tensor) -> float:
-    x = x.to("cpu", torch.float32)
-    x_ref = x_ref.to("cpu", torch.float32)
-    return ((x - x_ref).abs().max() / max(1.0, x_ref.abs().max().item())).item()
+# Largest rounding error of a stored value x relative to |x|: a 16-bit
+# gradient cannot hold x more closely than that.
+STORAGE = {torch.float32: 2.0**-24, torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
+
+
+def grad_bound(x_ref: torch.Tensor, dtype) -> float:
+    """The north-star absolute bound on top of the output's own storage
+    rounding at the largest reference gradient (which alone reaches 2e-2 in
+    bf16 once |x| >= 8: bench-shape dv reaches 7.7 and 16.5)."""
+    return TOL[dtype] + STORAGE[dtype] * x_ref.abs().max().item()
 
 
 def _check(grads, refs, dtype, what=""):
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
-        e = grad_err(g, r)
-        assert e <= TOL[dtype], f"{what} {name} err {e}"
+        r = r.to("cpu", torch.float32)
+        e = (g.to("cpu", torch.float32) - r).abs().max().item()
+        bound = grad_bound(r, dtype)
+        assert e <= bound, f"{what} {name} err {e} > {bound} (max |ref| {r.abs().max().item()})"
 
 
 def _case(b, tq, tk, hq, hkv, d, dtype, *, causal, window=-1, alibi=False, rope=False, seed=0):
@@ -120,8 +129,7 @@ def test_backward_workgroup_order_partial_chunks():
 
 def test_backward_rows_without_keys():
     """Lq > Lk with causal: the first Lq - Lk rows see no key; their o is 0
-    and they contribute nothing (checked against the float64 brute force,
-    since SDPA itself returns NaN there)."""
+    and they contribute nothing (checked against the float64 brute force)."""
     b, tq, tk, hq, hkv, d = 1, 12, 8, 2, 1, 64
     q, k, v = (_rand(s, torch.float32, i) for i, s in enumerate([(b, tq, hq, d), (b, tk, hkv, d), (b, tk, hkv, d)]))
     d_o = _rand((b, tq, hq, d), torch.float32, 9, std=1.0)
@@ -129,7 +137,7 @@ def test_backward_rows_without_keys():
     dq, dk, dv = ops.attention_prefill_bwd(q.to(DEV), k.to(DEV), v.to(DEV), o, lse, d_o.to(DEV), causal=True)
     bq, bk, bv = brute.attention_backward(q.numpy(), k.numpy(), v.numpy(), d_o.numpy(), causal=True)
     for g, r in ((dq, bq), (dk, bk), (dv, bv)):
-        assert grad_err(g, torch.from_numpy(r)) <= 1e-4
+        assert (g.cpu().double() - torch.from_numpy(r)).abs().max().item() <= 1e-4
     assert torch.all(dq[:, : tq - tk].cpu() == 0)
 
 
@@ -242,5 +250,7 @@ def test_gqa_layer_training_step_matches_cpu_reference():
     y_ref = o.reshape(2, t, -1) @ sd["wo.weight"].T
     y_ref.backward(gy)
     for n, g in grads.items():
+        # parameter gradients sum over every row: compared relative to their size
         r = sd[n].grad
-        assert grad_err(g, r) <= 1e-4, f"{n}"
+        e = ((g.cpu().float() - r).abs().max() / max(1.0, r.abs().max().item())).item()
+        assert e <= 1e-4, f"{n}"

@@ -63,15 +63,6 @@ def test_flashattention_doc_ids(with_rope):
     assert max_err(o, o_ref) <= 2e-2
 
 
-def test_flashattention_refuses_what_it_cannot_run():
-    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16, device=DEV)
-    fa = FlashAttention()
-    with pytest.raises(NotImplementedError):
-        fa(q, q, q, causal=True, base_attn_mask=torch.ones(1, 1, 8, 8, dtype=torch.bool, device=DEV))
-    with pytest.raises(NotImplementedError):
-        fa(q, q, q, causal=True, window_size=(4, 4))
-
-
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_kvcache_generate_loop_matches_full_causal(dtype):
     """Prompt through the cache (chunked prefill), then token-by-token decode:

@@ -8,7 +8,9 @@ import math
 import pytest
 import torch
 
+from goda_amd import ops
 from goda_amd import workloads as wl
+from goda_amd.mint.kvcache import KVCache
 from goda_amd.mint.nn import FlashAttention, LinearScaledRoPE, RoPE, alibi_slopes
 from goda_amd.mint.nn.flashattn import _segments
 from oracle import attention as ref
@@ -67,12 +69,64 @@ def test_workload_seeds_are_deterministic():
     assert lens.min() >= 1024 and lens.max() <= 32768 and lens.dtype == torch.int32
 
 
-def test_flashattention_refuses_cpu_and_unsupported_masks():
+def test_flashattention_refuses_cpu_tensors():
+    """No CPU path: a base mask and a right window are accepted (the right
+    window ignored, as in the reference's SDPA branch) and still reach the
+    GPU-only kernels, which refuse CPU tensors."""
     fa = FlashAttention()
     q = torch.zeros(1, 4, 2, 64)
     with pytest.raises(ValueError, match="GPU tensor"):
         fa(q, q, q, causal=True)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="GPU tensor"):
         fa(q, q, q, causal=True, base_attn_mask=torch.ones(1, 1, 4, 4, dtype=torch.bool))
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="GPU tensor"):
         fa(q, q, q, causal=True, window_size=(2, 2))
+
+
+@pytest.mark.parametrize("shape", [(3, 1, 1, 70), (3, 1, 5, 70), (3, 4, 5, 70), (5, 70), (3, 1, 5, 1), (70,)])
+def test_pack_mask_bits_match_the_boolean_mask(shape):
+    """ops.pack_mask (torch ops, runs on the CPU too): bit j % 32 of word
+    j // 32 of row (b, h, i) is the mask at key j; broadcast dimensions get a
+    zero stride; keys past the mask's own key count read as hidden."""
+    b, hq, tq, tk = 3, 4, 5, 70
+    g = torch.Generator().manual_seed(1)
+    m = torch.rand(shape, generator=g) < 0.5
+    pm = ops.pack_mask(m, b, hq, tq, tk + 10, "cpu")
+    assert pm.bits.dtype == torch.int32 and pm.bits.shape[-1] == 2 * ((tk + 10 + 63) // 64)
+    full = m
+    while full.dim() < 4:
+        full = full.unsqueeze(0)
+    full = full.expand(b, hq, tq, full.shape[-1] if full.shape[-1] != 1 else tk + 10)
+    words = pm.bits.reshape(-1).to(torch.int64) & 0xFFFFFFFF
+    for bb in range(b):
+        for h in range(hq):
+            for i in range(tq):
+                base = bb * pm.stride_b + h * pm.stride_h + i * pm.stride_q
+                for j in range(tk + 10):
+                    bit = bool((int(words[base + j // 32]) >> (j % 32)) & 1)
+                    want = bool(full[bb, h, i, j]) if j < full.shape[-1] else False
+                    assert bit == want, (bb, h, i, j)
+
+
+def test_pack_mask_rejects_non_boolean_and_bad_shapes():
+    with pytest.raises(ValueError, match="boolean"):
+        ops.pack_mask(torch.zeros(1, 1, 4, 4), 1, 2, 4, 4, "cpu")
+    with pytest.raises(ValueError, match="broadcast"):
+        ops.pack_mask(torch.ones(2, 1, 4, 4, dtype=torch.bool), 3, 2, 4, 4, "cpu")
+    with pytest.raises(ValueError, match="keys"):
+        ops.pack_mask(torch.ones(1, 1, 4, 9, dtype=torch.bool), 1, 2, 4, 8, "cpu")
+
+
+def test_kvcache_host_bound_rejects_overflow_before_any_launch():
+    """An append past max_seq_len fails on the host while the lengths are
+    known there (as the reference's slice assignment fails,
+    mint/kvcache/base.py:40-43), before any kernel is called."""
+    kv = KVCache(max_batch_size=2, max_seq_len=8, n_kv_heads=1, head_dim=64, dtype=torch.bfloat16, device="cpu")
+    k = torch.zeros(2, 9, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="max_seq_len"):
+        kv.append(k, k)
+    assert kv.len_bound == 0
+    kv.get_cache_tensors()  # the caller could now change the lengths
+    assert kv.len_bound is None
+    kv.reset()
+    assert kv.len_bound == 0

@@ -98,6 +98,82 @@ def test_doc_ids_match_brute_and_varlen():
     assert torch.allclose(o_v.reshape(b, t, hq, d), o_b, atol=1e-12)
 
 
+def _bool(shape, seed, p=0.7):
+    g = torch.Generator().manual_seed(seed)
+    return torch.rand(shape, generator=g) < p
+
+
+# base_attn_mask forms goda's callers pass (broadcast against [B, Hq, Tq, Tk])
+MASK_FORMS = ["keypad", "full", "per_head", "two_d"]
+
+
+def _mask_of(form, b, hq, tq, tk, seed):
+    if form == "keypad":  # SFT padding: [B, 1, 1, Tk]
+        m = _bool((b, 1, 1, tk), seed)
+    elif form == "full":
+        m = _bool((b, 1, tq, tk), seed)
+    elif form == "per_head":
+        m = _bool((b, hq, tq, tk), seed)
+    else:
+        m = _bool((tq, tk), seed)
+    return m
+
+
+@pytest.mark.parametrize("form", MASK_FORMS)
+@pytest.mark.parametrize("causal,window,alibi", [(True, -1, False), (False, -1, False), (True, 2, True), (False, -1, True)])
+def test_base_mask_matches_brute(form, causal, window, alibi):
+    b, tq, tk, hq, hkv, d = 2, 5, 8, 4, 2, 8
+    q, k, v = _rand((b, tq, hq, d), 31), _rand((b, tk, hkv, d), 32), _rand((b, tk, hkv, d), 33)
+    m = _mask_of(form, b, hq, tq, tk, 34)
+    slopes = torch.tensor(ref.alibi_slopes(hq), dtype=F64) if alibi else None
+    o = ref.attention(q, k, v, causal=causal, window_size=(window, -1), alibi_slopes=slopes, base_attn_mask=m,
+                      dtype=F64)
+    o_b, lse_b = _brute(q, k, v, causal=causal, window_left=window, mask=m.numpy(),
+                        slopes=None if slopes is None else slopes.numpy())
+    assert torch.allclose(o, o_b, atol=1e-12)
+    o_r, lse_r = ref.attention_rows(q, k, v, torch.arange(tq), causal=causal, window_left=window,
+                                    alibi_slopes=slopes, base_attn_mask=m, dtype=F64)
+    assert torch.allclose(torch.nan_to_num(o_r), o_b, atol=1e-12)
+    assert torch.equal(torch.isinf(lse_r), torch.isinf(lse_b))
+    fin = torch.isfinite(lse_b)
+    assert torch.allclose(lse_r[fin], lse_b[fin], atol=1e-12)
+
+
+def test_base_mask_rows_with_no_key_give_zero():
+    """A row the mask hides entirely comes out as 0 with lse = -inf in the
+    brute force, and the restatement (this torch's SDPA) agrees."""
+    b, tq, tk, hq, d = 1, 4, 6, 2, 8
+    q, k, v = _rand((b, tq, hq, d), 35), _rand((b, tk, hq, d), 36), _rand((b, tk, hq, d), 37)
+    m = torch.ones(b, 1, tq, tk, dtype=torch.bool)
+    m[0, 0, 2] = False
+    o_b, lse_b = _brute(q, k, v, causal=False, mask=m.numpy())
+    assert torch.all(o_b[0, 2] == 0) and torch.all(torch.isinf(lse_b[0, :, 2]))
+    o = ref.attention(q, k, v, causal=False, base_attn_mask=m, dtype=F64)
+    assert torch.allclose(o, o_b, atol=1e-12)
+
+
+def test_base_mask_and_doc_ids_compose_as_a_conjunction():
+    b, t, hq, hkv, d = 2, 7, 2, 1, 8
+    q, k, v = _rand((b, t, hq, d), 38), _rand((b, t, hkv, d), 39), _rand((b, t, hkv, d), 40)
+    doc = torch.tensor([[0, 0, 0, 1, 1, 1, 1], [3, 3, 4, 4, 4, 5, 5]])
+    m = _bool((b, 1, 1, t), 41)
+    o = ref.attention(q, k, v, causal=True, doc_ids=doc, base_attn_mask=m, dtype=F64)
+    both = (doc[:, None, :, None] == doc[:, None, None, :]) & m
+    o_b, _ = _brute(q, k, v, causal=True, mask=both.numpy())
+    assert torch.allclose(o, o_b, atol=1e-12)
+
+
+def test_planted_transposed_mask_is_caught():
+    """Reading the mask as [.., key, query] instead of [.., query, key] fails
+    the brute-force comparison."""
+    b, t, hq, d = 1, 6, 2, 8
+    q, k, v = _rand((b, t, hq, d), 42), _rand((b, t, hq, d), 43), _rand((b, t, hq, d), 44)
+    m = _bool((b, 1, t, t), 45, p=0.5)
+    o_wrong = ref.attention(q, k, v, causal=False, base_attn_mask=m.transpose(-1, -2), dtype=F64)
+    o_b, _ = _brute(q, k, v, causal=False, mask=m.numpy())
+    assert not torch.allclose(torch.nan_to_num(o_wrong), o_b, atol=1e-3)
+
+
 def test_causal_square_equals_is_causal():
     """With Lq == Lk and no other mask, goda's explicit boolean mask equals
     SDPA's is_causal=True (mint/nn/flashattn.py:245-273)."""
@@ -331,6 +407,10 @@ GRAD_CASES = [
     ("noncausal_alibi", 3, 4, 2, 1, 3, dict(causal=False, slopes=np.array([0.5, 0.25]))),
     ("causal_empty_rows", 6, 4, 2, 1, 3, dict(causal=True)),
     ("doc_ids", 5, 5, 2, 2, 3, dict(causal=True, doc_ids=np.array([[0, 0, 1, 1, 1]]))),
+    # base_attn_mask with a row it hides entirely (row 1) and a per-head form
+    ("base_mask", 4, 5, 2, 1, 3, dict(causal=False, mask=np.array(
+        [[[[1, 0, 1, 1, 0], [0, 0, 0, 0, 0], [1, 1, 0, 1, 1], [0, 1, 1, 0, 1]],
+          [[1, 1, 1, 0, 0], [0, 0, 0, 0, 0], [0, 1, 1, 1, 1], [1, 0, 0, 1, 1]]]], dtype=bool))),
 ]
 
 
@@ -380,6 +460,19 @@ def test_autograd_oracle_matches_brute_backward(b, tq, tk, hq, hkv, d, causal, w
         q.numpy(), k.numpy(), v.numpy(), d_o.numpy(), causal=causal, window_left=window,
         slopes=None if slopes is None else slopes.numpy(),
     )
+    assert np.abs(dq.numpy() - bq).max() < 1e-10
+    assert np.abs(dk.numpy() - bk).max() < 1e-10
+    assert np.abs(dv.numpy() - bv).max() < 1e-10
+
+
+@pytest.mark.parametrize("form", MASK_FORMS)
+def test_autograd_oracle_with_base_mask_matches_brute_backward(form):
+    b, tq, tk, hq, hkv, d = 2, 5, 7, 4, 2, 8
+    q, k, v = _rand((b, tq, hq, d), 46), _rand((b, tk, hkv, d), 47), _rand((b, tk, hkv, d), 48)
+    d_o = _rand((b, tq, hq, d), 49)
+    m = _mask_of(form, b, hq, tq, tk, 50)
+    dq, dk, dv = ref.attention_grads(q, k, v, d_o, causal=True, base_attn_mask=m, dtype=F64)
+    bq, bk, bv = brute.attention_backward(q.numpy(), k.numpy(), v.numpy(), d_o.numpy(), causal=True, mask=m.numpy())
     assert np.abs(dq.numpy() - bq).max() < 1e-10
     assert np.abs(dk.numpy() - bk).max() < 1e-10
     assert np.abs(dv.numpy() - bv).max() < 1e-10
@@ -436,3 +529,25 @@ def test_planted_rms_norm_without_one_plus_is_caught():
     lib = torch.nn.functional.rms_norm(x, (16,), weight=1.0 + scale, eps=1e-6)
     assert not torch.allclose(wrong, lib, atol=1e-3)
     assert torch.allclose(ref.rms_norm(x, scale, 1e-6), lib, atol=1e-12)
+
+
+@pytest.mark.parametrize("causal,alibi,tq,tk", [(True, False, 13, 13), (True, True, 9, 17), (False, False, 11, 7),
+                                                (False, True, 6, 6)])
+def test_chunked_grads_match_autograd_oracle(causal, alibi, tq, tk):
+    """The row-chunked backward (used on full-size shapes) equals the autograd
+    oracle for one (sequence, KV head) group: chunk sizes that do and do not
+    divide the rows, bottom-right alignment, ALiBi, and sampled dq rows."""
+    g, d = 3, 8
+    q, k, v = _rand((1, tq, g, d), 61), _rand((1, tk, 1, d), 62), _rand((1, tk, 1, d), 63)
+    d_o = _rand((1, tq, g, d), 64)
+    slopes = torch.tensor([0.5, 0.25, 0.125], dtype=F64) if alibi else None
+    dq, dk, dv = ref.attention_grads(q, k, v, d_o, causal=causal, alibi_slopes=slopes, dtype=F64)
+    for chunk in (1, 4, 64):
+        cq, ck, cv = ref.attention_grads_chunked(q[0], k[0, :, 0], v[0, :, 0], d_o[0], causal=causal,
+                                                 alibi_slopes=slopes, chunk=chunk, dtype=F64)
+        assert torch.allclose(cq, dq[0], atol=1e-10)
+        assert torch.allclose(ck, dk[0, :, 0], atol=1e-10) and torch.allclose(cv, dv[0, :, 0], atol=1e-10)
+    rows = torch.tensor([0, tq // 2, tq - 1])
+    cq, _, _ = ref.attention_grads_chunked(q[0], k[0, :, 0], v[0, :, 0], d_o[0], causal=causal, alibi_slopes=slopes,
+                                           rows=rows, chunk=2, dtype=F64)
+    assert torch.allclose(cq, dq[0, rows], atol=1e-10)
