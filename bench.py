@@ -8,7 +8,10 @@ inputs already resident in HBM:
                     D=128, RoPE base 10000 fused (K pre-pass + attention kernel)
   decode            cfg4: one decode token for 64 sequences, Hq=32, Hkv=8,
                     D=128, cache [64, 8, 32768, 128], lengths U[1024, 32768]
-  also reported     cfg3 (MQA + ALiBi, D=256) and cfg5 (ragged mix, D=256)
+  also reported     cfg3 (MQA + ALiBi, D=256) and cfg5 (ragged mix, D=256: the
+                    packed prefill and the decode batch as one step, the decode
+                    on a second stream of the same priority so it runs beside
+                    the prefill; also each alone)
 
 Throughputs use algorithmic work only (causal QK^T + PV flops over visible
 pairs; each valid cached K/V byte once plus q and o). The `roofline` objects
@@ -180,6 +183,64 @@ def bench_decode(w, steps, warmup):
     }
 
 
+def bench_mix(mix, steps, warmup):
+    """cfg5 as one step: the packed prefill on the current stream and the
+    48-sequence decode on a second stream (default priority), forked from and
+    joined back into the current stream, so the HBM-bound decode can run in
+    the MFMA-bound prefill's shadow. Also times each part alone."""
+    import torch
+
+    from goda_amd import ops
+    from goda_amd import workloads as wl
+
+    pin = wl.prefill_inputs(mix.prefill, "cuda")
+    din = wl.decode_inputs(mix.decode, "cuda")
+    pl = _prefill_launch(mix.prefill, pin, ops)
+    dl = _decode_launch(mix.decode, din, ops)
+    p_ms, p_kms = _time_steps(pl, steps, warmup)
+    d_ms, d_kms = _time_steps(dl, steps, warmup)
+    main_s = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    fork = [torch.cuda.Event() for _ in range(steps + warmup)]
+    join = [torch.cuda.Event() for _ in range(steps + warmup)]
+
+    def step(i):
+        fork[i].record(main_s)
+        pl()
+        side.wait_event(fork[i])
+        with torch.cuda.stream(side):
+            dl()
+        join[i].record(side)
+        main_s.wait_event(join[i])
+
+    for i in range(warmup):
+        step(steps + i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    mix_ms = t0.elapsed_time(t1) / steps
+    flops = wl.prefill_flops(mix.prefill, pin.get("lengths"))
+    nbytes = wl.decode_bytes(mix.decode, din["lengths"])
+    roof_ms = (flops / (wl.BF16_PEAK_TFLOPS * 1e12) + nbytes / (wl.HBM_PEAK_GBPS * 1e9)) * 1e3
+    del pl, dl, pin, din
+    return {
+        "workload": mix.name,
+        "prefill_flops": flops,
+        "decode_bytes": nbytes,
+        "mix_ms": mix_ms,
+        "roofline_ms": roof_ms,
+        "prefill_ms": p_ms,
+        "prefill_kernel_ms": p_kms,
+        "decode_ms": d_ms,
+        "decode_kernel_ms": d_kms,
+    }
+
+
 def _median_time(fn, reps: int) -> float:
     fn()  # warm-up
     ts = []
@@ -198,7 +259,7 @@ def cpu_baseline_prefill(w, reps: int = 3):
     from goda_amd import workloads as wl
     from oracle import attention as ref
 
-    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(os.cpu_count() or 1)
     inp = wl.prefill_inputs(w, "cpu")
     pos = torch.arange(w.seqlen)
 
@@ -241,7 +302,7 @@ def cpu_baseline_decode(w, nseq: int = 8, reps: int = 3):
         vc = inp["v_cache"][:nseq, :L].cpu()
     del inp
     torch.cuda.empty_cache()
-    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(os.cpu_count() or 1)
 
     def run():
         return ref.decode_attention_sdpa(q, kc, vc, lens, dtype=w.dtype)
@@ -254,6 +315,7 @@ def cpu_baseline_decode(w, nseq: int = 8, reps: int = 3):
         "kind": "port",
         "sample": f"first {nseq} of {w.batch} sequences of {w.name} (keys {int(lens.sum())}), "
         f"median of {reps}: {sec:.3f} s",
+        "os_cpu_count": os.cpu_count(),
     }
 
 
@@ -289,7 +351,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["prefill", "decode", "backward"], default=None)
+    ap.add_argument("--only", choices=["prefill", "decode", "backward", "cfg3", "cfg5"], default=None)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -320,14 +382,13 @@ def main() -> int:
         d4 = bench_decode(wl.CFG4, steps, warmup)
         _log(f"  {d4}")
         out["cfg4"] = d4
-    if args.only is None:
+    if args.only in (None, "cfg3"):
         _log("bench: cfg3 prefill")
         out["cfg3"] = bench_prefill(wl.CFG3, steps, warmup)
         _log(f"  {out['cfg3']}")
+    if args.only in (None, "cfg5"):
         _log("bench: cfg5 mix")
-        p5 = bench_prefill(wl.CFG5.prefill, steps, warmup)
-        d5 = bench_decode(wl.CFG5.decode, steps, warmup)
-        out["cfg5"] = {"prefill": p5, "decode": d5}
+        out["cfg5"] = bench_mix(wl.CFG5, steps, warmup)
         _log(f"  {out['cfg5']}")
     if args.only in (None, "backward"):
         _log("bench: cfg2 backward")
@@ -423,14 +484,18 @@ def main() -> int:
         line["cfg3"] = {"tflops": round(c3["tflops"], 2), "mfma_peak_frac": round(c3["tflops"] / peak_tf, 4),
                         "ms_per_step": round(c3["ms_per_step"], 4)}
     if "cfg5" in out:
-        p5, d5 = out["cfg5"]["prefill"], out["cfg5"]["decode"]
+        m5 = out["cfg5"]
         line["cfg5"] = {
-            "prefill_tflops": round(p5["tflops"], 2),
-            "prefill_mfma_frac": round(p5["tflops"] / peak_tf, 4),
-            "prefill_ms": round(p5["ms_per_step"], 4),
-            "decode_tokens_per_s": round(d5["tokens_per_s"], 1),
-            "decode_hbm_frac": round(d5["gbps"] / peak_bw, 4),
-            "decode_ms": round(d5["ms_per_step"], 4),
+            "mix_ms": round(m5["mix_ms"], 4),
+            "serial_ms": round(m5["prefill_ms"] + m5["decode_ms"], 4),
+            "roofline_ms": round(m5["roofline_ms"], 4),
+            "roofline_frac": round(m5["roofline_ms"] / m5["mix_ms"], 4),
+            "prefill_tflops": round(m5["prefill_flops"] / (m5["prefill_ms"] * 1e-3) / 1e12, 2),
+            "prefill_mfma_frac": round(m5["prefill_flops"] / (m5["prefill_ms"] * 1e-3) / 1e12 / peak_tf, 4),
+            "prefill_ms": round(m5["prefill_ms"], 4),
+            "decode_tokens_per_s": round(wl.CFG5.decode.batch / (m5["decode_ms"] * 1e-3), 1),
+            "decode_hbm_frac": round(m5["decode_bytes"] / (m5["decode_ms"] * 1e-3) / 1e9 / peak_bw, 4),
+            "decode_ms": round(m5["decode_ms"], 4),
         }
     if "bwd" in out:
         bw = out["bwd"]

@@ -641,7 +641,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     // probabilities (rounded to the operand type) and their row sums
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      float lsum = l_run[nt];
+      // Four independent row-sum chains (one per dot-product slot) instead of
+      // one chain of 2*MT*4 dependent dot products: cfg2 +1.1-1.5%.
+      float ls[4] = {l_run[nt], 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -650,11 +652,11 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
           for (int e = 0; e < 8; ++e) pv[e] = (T)fast_exp2(s[mt][nt][8 * h + e]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) lsum = dot2_ones(pv, i, lsum);
+          for (int i = 0; i < 4; ++i) ls[i] = dot2_ones(pv, i, ls[i]);
           pf[nt][2 * mt + h] = pv;
         }
       }
-      l_run[nt] = lsum;
+      l_run[nt] = (ls[0] + ls[1]) + (ls[2] + ls[3]);
     }
   };
 
@@ -663,13 +665,14 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     const v8* vp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES + TG::K_CHUNKS * TG::CHB) +
                    hi * D + l32;
 #pragma unroll
-    for (int ks2 = 0; ks2 < KS2; ++ks2)
+    for (int ks2 = 0; ks2 < KS2; ++ks2) {
 #pragma unroll
       for (int md = 0; md < MD; ++md) {
         const v8 av = vp[ks2 * 2 * D + md * 32];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) oacc[md][nt] = mfma32(av, pf[nt][ks2], oacc[md][nt]);
       }
+    }
   };
 
   // MFMA half of a step: O += P(j)V(j), then S(j+1) = K(j+1)Q^T (tile j again,

@@ -1,0 +1,105 @@
+"""Summaries of rocprofv3 CSV output for the kernels of this package.
+
+    python -m goda_amd.tracestats trace <kernel_trace.csv> --kernel REGEX [--last N]
+    python -m goda_amd.tracestats pmc <counter_collection.csv> [--kernel REGEX] [--last N]
+
+`trace` reads a `rocprofv3 --kernel-trace --output-format csv` file and prints,
+per kernel name matching REGEX, the dispatch count and the mean / median /
+min / max duration in microseconds — over the LAST N dispatches when `--last`
+is given (a bench run launches its W warm-up steps first, so `--last K`
+selects exactly the K timed steps). `pmc` reads a `rocprofv3 --pmc` file and
+prints each counter's mean per dispatch (summed over the XCD / SE instances
+the CSV lists separately), plus the matrix-core utilisation when
+SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE are both present.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import re
+import statistics
+import sys
+from collections import defaultdict
+
+# MI355X: 8 XCDs x 32 CUs x 4 SIMDs; GRBM_GUI_ACTIVE is summed over the XCDs.
+SIMDS = 1024
+XCDS = 8
+
+
+def kernel_trace(path: str, kernel: str, last: int | None) -> list[dict]:
+    pat = re.compile(kernel)
+    by_name: dict[str, list[tuple[int, float]]] = defaultdict(list)
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r.get("Kernel_Name", "")
+            if not pat.search(name):
+                continue
+            start, end = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            by_name[name].append((start, (end - start) / 1e3))
+    out = []
+    for name, rows in by_name.items():
+        rows.sort()
+        durs = [d for _, d in rows]
+        if last:
+            durs = durs[-last:]
+        out.append({
+            "kernel": name,
+            "dispatches": len(rows),
+            "summarised": len(durs),
+            "mean_us": statistics.fmean(durs),
+            "median_us": statistics.median(durs),
+            "min_us": min(durs),
+            "max_us": max(durs),
+        })
+    return out
+
+
+def counters(path: str, kernel: str | None, last: int | None) -> dict[str, float]:
+    pat = re.compile(kernel) if kernel else None
+    per: dict[tuple[int, str], float] = defaultdict(float)
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if pat and not pat.search(r.get("Kernel_Name", "")):
+                continue
+            per[(int(r["Dispatch_Id"]), r["Counter_Name"])] += float(r["Counter_Value"])
+    dispatches = sorted({d for d, _ in per})
+    if last:
+        dispatches = dispatches[-last:]
+    keep = set(dispatches)
+    vals: dict[str, list[float]] = defaultdict(list)
+    for (d, c), v in per.items():
+        if d in keep:
+            vals[c].append(v)
+    avg = {c: statistics.fmean(v) for c, v in vals.items()}
+    avg["dispatches"] = float(len(dispatches))
+    g = avg.get("GRBM_GUI_ACTIVE")
+    if g and "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+        avg["mfma_busy_frac"] = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (g / XCDS * SIMDS)
+    return avg
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(prog="python -m goda_amd.tracestats")
+    sub = ap.add_subparsers(dest="mode", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("csv")
+    t.add_argument("--kernel", default=".")
+    t.add_argument("--last", type=int, default=None)
+    p = sub.add_parser("pmc")
+    p.add_argument("csv")
+    p.add_argument("--kernel", default=None)
+    p.add_argument("--last", type=int, default=None)
+    a = ap.parse_args(argv)
+    if a.mode == "trace":
+        for s in kernel_trace(a.csv, a.kernel, a.last):
+            print(f"{s['kernel'][:90]}\n  dispatches {s['dispatches']}, summarised {s['summarised']}: "
+                  f"mean {s['mean_us']:.1f} us, median {s['median_us']:.1f}, min {s['min_us']:.1f}, max {s['max_us']:.1f}")
+    else:
+        for c, v in sorted(counters(a.csv, a.kernel, a.last).items()):
+            print(f"{c:34s} {v:.6g}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
