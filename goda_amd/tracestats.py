@@ -2,6 +2,7 @@
 
     python -m goda_amd.tracestats trace <kernel_trace.csv> --kernel REGEX [--last N]
     python -m goda_amd.tracestats pmc <counter_collection.csv> [--kernel REGEX] [--last N]
+    python -m goda_amd.tracestats copy [--mib 1100] [--reps 3]
 
 `trace` reads a `rocprofv3 --kernel-trace --output-format csv` file and prints,
 per kernel name matching REGEX, the dispatch count and the mean / median /
@@ -10,7 +11,11 @@ is given (a bench run launches its W warm-up steps first, so `--last K`
 selects exactly the K timed steps). `pmc` reads a `rocprofv3 --pmc` file and
 prints each counter's mean per dispatch (summed over the XCD / SE instances
 the CSV lists separately), plus the matrix-core utilisation when
-SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE are both present.
+SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE are both present. `copy` runs a
+plain device-to-device copy of a known size (torch's copy kernel), the
+calibration for the FETCH_SIZE / WRITE_SIZE byte counters: profiled under the
+same counter, it shows what the counter reports for `mib` MiB read and `mib`
+MiB written.
 """
 
 from __future__ import annotations
@@ -79,6 +84,18 @@ def counters(path: str, kernel: str | None, last: int | None) -> dict[str, float
     return avg
 
 
+def copy_run(mib: int, reps: int) -> None:
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copied {mib} MiB {reps} times", flush=True)
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(prog="python -m goda_amd.tracestats")
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -90,7 +107,13 @@ def main(argv: list[str] | None = None) -> int:
     p.add_argument("csv")
     p.add_argument("--kernel", default=None)
     p.add_argument("--last", type=int, default=None)
+    c = sub.add_parser("copy")
+    c.add_argument("--mib", type=int, default=1100)
+    c.add_argument("--reps", type=int, default=3)
     a = ap.parse_args(argv)
+    if a.mode == "copy":
+        copy_run(a.mib, a.reps)
+        return 0
     if a.mode == "trace":
         for s in kernel_trace(a.csv, a.kernel, a.last):
             print(f"{s['kernel'][:90]}\n  dispatches {s['dispatches']}, summarised {s['summarised']}: "
