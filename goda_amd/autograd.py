@@ -11,9 +11,11 @@ boolean mask) are treated as constants.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
-from . import ops
+from . import headdim, ops
 
 
 class PrefillAttention(torch.autograd.Function):
@@ -32,6 +34,8 @@ class PrefillAttention(torch.autograd.Function):
 
 
 def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **options) -> torch.Tensor:
+    if not headdim.is_native(q.shape[-1]):
+        return _padded(q, k, v, options)
     m = options.get("attn_mask")
     if m is not None and not isinstance(m, ops.PackedMask) and q.dim() == 4:
         # Packed once, shared by the forward and the backward.
@@ -40,3 +44,68 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **optio
         options.pop("return_lse", None)
         return PrefillAttention.apply(q, k, v, options)
     return ops.attention_prefill(q, k, v, **options)
+
+
+def _row_positions(cu: torch.Tensor, total: int) -> torch.Tensor:
+    """Position of each packed row inside its sequence (rows of sequence b
+    are cu[b] .. cu[b+1]-1)."""
+    rows = torch.arange(total, device=cu.device)
+    seq = torch.searchsorted(cu[1:].to(torch.int64), rows, right=True)
+    return rows - cu.to(torch.int64)[seq]
+
+
+def _padded(q, k, v, options: dict) -> torch.Tensor:
+    """A head dim the kernels do not instantiate (see goda_amd.headdim): the
+    fused QK-RMSNorm and RoPE options run as torch ops at the positions the
+    kernels would use, then q, k, v are zero-padded to the next instantiated
+    head dim, attended with the 1/sqrt(D) scale of the real head dim, and the
+    output sliced back; gradients flow through the pad and the slice."""
+    opts = dict(options)
+    d = q.shape[-1]
+    dp = headdim.padded(d)
+    qn, kn = opts.pop("q_norm_weight", None), opts.pop("k_norm_weight", None)
+    eps = opts.pop("norm_eps", 1e-6)
+    if qn is not None:
+        q = headdim.rms_norm(q, qn, eps)
+    if kn is not None:
+        k = headdim.rms_norm(k, kn, eps)
+    cos, sin = opts.pop("rope_cos", None), opts.pop("rope_sin", None)
+    rq, rk = opts.pop("rope_q", False), opts.pop("rope_k", False)
+    qo, ko = int(opts.pop("rope_q_offset", 0)), int(opts.pop("rope_k_offset", 0))
+    pabs = bool(opts.pop("rope_pos_abs", False))
+    if (rq or rk) and cos is None:
+        raise ValueError("goda_amd: rope_q/rope_k need rope_cos and rope_sin")
+    varlen = opts.get("cu_seqlens_q") is not None
+    if rq or rk:
+        cos = cos.reshape(-1, d // 2).float()
+        sin = sin.reshape(-1, d // 2).float()
+        if varlen:
+            cu_q, cu_k = opts["cu_seqlens_q"], opts["cu_seqlens_k"]
+            iq = _row_positions(cu_q, q.shape[0])
+            jk = _row_positions(cu_k, k.shape[0])
+            if rq:
+                seq = torch.searchsorted(cu_q[1:].to(torch.int64), torch.arange(q.shape[0], device=q.device), right=True)
+                lk = (cu_k[1:] - cu_k[:-1]).to(torch.int64)[seq]
+                lq = (cu_q[1:] - cu_q[:-1]).to(torch.int64)[seq]
+                pos = qo + iq if pabs else qo + (lk - lq) + iq
+                q = headdim.rotate(q[None], cos, sin, pos[None])[0]
+            if rk:
+                k = headdim.rotate(k[None], cos, sin, (ko + jk)[None])[0]
+        else:
+            tq, tk = q.shape[1], k.shape[1]
+            if rq:
+                i = torch.arange(tq, device=q.device)
+                used = opts.get("seqused_k")
+                if pabs:
+                    pos = qo + i
+                elif used is not None:
+                    pos = qo + (used.to(torch.int64)[:, None] - tq) + i[None]
+                else:
+                    pos = qo + (tk - tq) + i
+                q = headdim.rotate(q, cos, sin, pos)
+            if rk:
+                k = headdim.rotate(k, cos, sin, ko + torch.arange(tk, device=k.device))
+    if opts.get("softmax_scale") is None:
+        opts["softmax_scale"] = 1.0 / math.sqrt(d)
+    o = attention_prefill(headdim.pad(q, dp), headdim.pad(k, dp), headdim.pad(v, dp), **opts)
+    return o[..., :d]

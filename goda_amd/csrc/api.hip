@@ -55,7 +55,9 @@ int32_t check_prefill(const goda_prefill_args* a, bool need_ptrs) {
     return fail(GODA_ERR_INVALID_ARG, "prefill: heads_q %d is not a multiple of heads_kv %d", a->heads_q,
                 a->heads_kv);
   if (!head_dim_ok(a->head_dim))
-    return fail(GODA_ERR_UNSUPPORTED, "prefill: head_dim %d not in {64, 128, 256}", a->head_dim);
+    return fail(GODA_ERR_UNSUPPORTED,
+                "prefill: head_dim %d not in {64, 128, 256} (goda_amd's Python layers zero-pad other head dims)",
+                a->head_dim);
   if ((a->cu_seqlens_q == nullptr) != (a->cu_seqlens_k == nullptr))
     return fail(GODA_ERR_INVALID_ARG, "prefill: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
   if (!(a->softmax_scale > 0.f))

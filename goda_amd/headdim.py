@@ -1,0 +1,62 @@
+"""Head dims the kernels do not instantiate.
+
+The HIP kernels are built for head_dim 64, 128 and 256; goda's eager path
+takes any head dim (mint/nn/flashattn.py:156-172) and its Triton kernel any
+power of two (kernels_/flash_attn_mqa/cuda.py:479-481). For another D <= 256
+the drop-in layers zero-pad q, k and v along the head dim to the next
+instantiated size Dp and slice the result back: a zero column adds nothing to
+any score q.k and gives a zero output column, so with the softmax scale kept
+at 1/sqrt(D) the first D output columns are exactly the D-wide attention, and
+the gradients of the padded inputs are those of the originals plus zero
+columns. What depends on D itself — the half-split RoPE pairing
+(mint/nn/pos.py:90-98) and the RMSNorm mean (mint/nn/norm.py:17-27) — is
+applied with torch ops before the padding instead of inside the kernels.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F  # noqa: N812
+
+NATIVE = (64, 128, 256)
+
+
+def padded(d: int) -> int:
+    """The instantiated head dim a D-wide head runs at (D itself if native)."""
+    for n in NATIVE:
+        if d <= n:
+            return n
+    raise ValueError(f"goda_amd: head_dim {d} > 256 is not supported")
+
+
+def is_native(d: int) -> bool:
+    return d in NATIVE
+
+
+def pad(x: torch.Tensor, dp: int) -> torch.Tensor:
+    """Zero-pad the last dim of x to dp (differentiable)."""
+    d = x.shape[-1]
+    return x if d == dp else F.pad(x, (0, dp - d))
+
+
+def rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    """goda's half-split RoPE (mint/nn/pos.py:90-98) of x [B, T, H, D] at
+    integer positions [T] or [B, T], computed in fp32 from the fp32 tables and
+    rounded once to x's dtype (the kernels' convention)."""
+    c = cos.to(x.device)[positions.to(x.device)]
+    s = sin.to(x.device)[positions.to(x.device)]
+    if c.dim() == 2:  # [T, D/2]
+        c, s = c[None, :, None, :], s[None, :, None, :]
+    else:  # [B, T, D/2]
+        c, s = c[:, :, None, :], s[:, :, None, :]
+    h = x.shape[-1] // 2
+    xf = x.float()
+    x1, x2 = xf[..., :h], xf[..., h:]
+    return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], dim=-1).to(x.dtype)
+
+
+def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
+    """goda's RMSNorm (mint/nn/norm.py:17-27): fp32, weight 1 + scale."""
+    x_f = x.float()
+    out = x_f * torch.rsqrt(x_f.pow(2).mean(dim=-1, keepdim=True) + eps) * (1.0 + scale.float().to(x.device))
+    return out.to(x.dtype)

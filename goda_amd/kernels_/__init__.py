@@ -11,7 +11,9 @@ and extend it compatibly:
     apply(Q, K, V, causal, tau, rope_cos, rope_sin, alibi_slopes, window_left)
     with fp32 tables [positions, D/2] (rotation at positions 0..T-1 for Q and
     K) and fp32 slopes [Hq];
-  - any T (the reference requires T to be a multiple of its block size).
+  - any T (the reference requires T to be a multiple of its block size);
+  - any head dim D <= 256: D outside {64, 128, 256} runs zero-padded to the
+    next one (goda_amd.headdim), RoPE then applied by torch ops.
 The forward saves O and the log-sum-exp M (natural log, fp32 [B, H, T]) like
 the reference (:571-575); the backward returns (dQ, dK, dV, None, ...) from
 them through `goda_attn_prefill_bwd` (:577-658), with dK/dV in K's and V's
@@ -22,10 +24,26 @@ from __future__ import annotations
 
 import torch
 
-from .. import ops
+from .. import headdim, ops
 
 
 class _FlashAttentionBase(torch.autograd.Function):
+    @classmethod
+    def apply(cls, Q, K, V, causal, tau, rope_cos=None, rope_sin=None, alibi_slopes=None, window_left=-1):  # noqa: N803
+        d = Q.shape[-1]
+        if headdim.is_native(d):
+            return super().apply(Q, K, V, causal, tau, rope_cos, rope_sin, alibi_slopes, window_left)
+        # zero-padded head dim (differentiable pad / slice around the kernel)
+        if rope_cos is not None:
+            t_q, t_k = Q.shape[2], K.shape[2]
+            cos, sin = rope_cos.float(), rope_sin.float()
+            Q = headdim.rotate(Q.transpose(1, 2), cos, sin, torch.arange(t_k - t_q, t_k)).transpose(1, 2)  # noqa: N806
+            K = headdim.rotate(K.transpose(1, 2), cos, sin, torch.arange(t_k)).transpose(1, 2)  # noqa: N806
+        dp = headdim.padded(d)
+        O = super().apply(headdim.pad(Q, dp), headdim.pad(K, dp), headdim.pad(V, dp), causal, tau,  # noqa: N806
+                          None, None, alibi_slopes, window_left)
+        return O[..., :d]
+
     @staticmethod
     def forward(ctx, Q, K, V, causal, tau, rope_cos=None, rope_sin=None, alibi_slopes=None, window_left=-1):  # noqa: N803
         if Q.dim() != 4 or K.dim() != 4 or V.dim() != 4:

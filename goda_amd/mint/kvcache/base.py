@@ -25,13 +25,16 @@ Additions:
     once the caller had the raw tensors, `get_cache_tensors()`, and could
     have changed them); attention over the cache sizes its launch by it
     instead of by `max_seq_len`.
+  - A head_dim the kernels do not instantiate is stored zero-padded to the
+    next one that they do (goda_amd.headdim); `k_cache` / `v_cache` stay
+    [B, L, H, head_dim] views, `cache_tensors()` gives the padded storage.
 """
 
 from __future__ import annotations
 
 import torch
 
-from ... import ops
+from ... import headdim, ops
 
 
 class KVCache:
@@ -50,9 +53,12 @@ class KVCache:
         self.head_dim = head_dim
         self.dtype = dtype
         self.device = device
-        store = (max_batch_size, n_kv_heads, max_seq_len, head_dim)
-        self.k_cache = torch.zeros(store, dtype=dtype, device=device).transpose(1, 2)
-        self.v_cache = torch.zeros(store, dtype=dtype, device=device).transpose(1, 2)
+        self.head_dim_padded = headdim.padded(head_dim)
+        store = (max_batch_size, n_kv_heads, max_seq_len, self.head_dim_padded)
+        self._k_store = torch.zeros(store, dtype=dtype, device=device).transpose(1, 2)
+        self._v_store = torch.zeros(store, dtype=dtype, device=device).transpose(1, 2)
+        self.k_cache = self._k_store[..., :head_dim]
+        self.v_cache = self._v_store[..., :head_dim]
         self.cache_seqlens = torch.zeros(max_batch_size, dtype=torch.int32, device=device)
         self.status = torch.zeros(1, dtype=torch.int32, device=device)
         self.len_bound: int | None = 0
@@ -82,11 +88,22 @@ class KVCache:
                     f"KVCache.append: {t} rows after up to {self.len_bound} cached exceed max_seq_len {self.max_seq_len}"
                 )
             self.len_bound += t
+        if self.head_dim_padded != self.head_dim:
+            # Norm and RoPE as torch ops at the kernel's positions, then rows
+            # zero-padded to the stored head dim.
+            if k_norm_weight is not None:
+                k = headdim.rms_norm(k, k_norm_weight, norm_eps)
+            if rope_cos is not None:
+                tt = torch.arange(t, device=k.device)
+                pos = int(start_pos) + tt if start_pos is not None else self.cache_seqlens[: k.shape[0], None].long() + tt
+                k = headdim.rotate(k, rope_cos.float(), rope_sin.float(), pos)
+            k, v = headdim.pad(k, self.head_dim_padded), headdim.pad(v, self.head_dim_padded)
+            rope_cos = rope_sin = k_norm_weight = None
         ops.kv_append(
             k,
             v,
-            self.k_cache,
-            self.v_cache,
+            self._k_store,
+            self._v_store,
             self.cache_seqlens,
             rope_cos=rope_cos,
             rope_sin=rope_sin,
@@ -133,8 +150,9 @@ class KVCache:
         return self.k_cache[:, :pos], self.v_cache[:, :pos]
 
     def cache_tensors(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """The raw tensors for this package's own kernels (keeps len_bound)."""
-        return self.k_cache, self.v_cache, self.cache_seqlens
+        """The storage for this package's own kernels, padded to
+        head_dim_padded (keeps len_bound)."""
+        return self._k_store, self._v_store, self.cache_seqlens
 
     def get_cache_tensors(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         # The caller may write the lengths: the host bound is no longer known.
@@ -147,8 +165,8 @@ class KVCache:
         self.len_bound = 0
 
     def clear(self) -> None:
-        self.k_cache.zero_()
-        self.v_cache.zero_()
+        self._k_store.zero_()
+        self._v_store.zero_()
         self.cache_seqlens.zero_()
         self.status.zero_()
         self.len_bound = 0

@@ -37,7 +37,9 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ... import autograd, ops
+import math
+
+from ... import autograd, headdim, ops
 from ..kvcache.base import KVCache
 
 
@@ -142,7 +144,7 @@ class FlashAttention(nn.Module):
         attention layer passes), q and the new k rotate at start_pos + t, as
         goda's RoPE(q, k, start_pos) does (mint/nn/pos.py:100-112); with
         start_pos None they rotate at their cache positions."""
-        b, tq = q.shape[0], q.shape[1]
+        b, tq, d = q.shape[0], q.shape[1], q.shape[-1]
         rope_kw = {}
         if rope is not None:
             rope_kw = dict(rope_cos=rope[0], rope_sin=rope[1], rope_q=True)
@@ -153,20 +155,36 @@ class FlashAttention(nn.Module):
                         **_norm_kwargs(qk_norm, q=False, k=True))
         k_cache, v_cache, seqlens = kv_cache.cache_tensors()
         used = seqlens[:b]
-        kw = _norm_kwargs(qk_norm, q=True, k=False)
-        kw.update(rope_kw)
+        native = headdim.is_native(d)
+        if native:
+            kw = _norm_kwargs(qk_norm, q=True, k=False)
+            kw.update(rope_kw)
+        else:
+            # A head dim without kernels: norm and RoPE as torch ops at the
+            # kernel's positions, q zero-padded like the stored rows, the
+            # real head dim's scale, the output sliced back.
+            if qk_norm is not None:
+                q = headdim.rms_norm(q, qk_norm[0], qk_norm[2])
+            if rope is not None:
+                tt = torch.arange(tq, device=q.device)
+                pos = int(start_pos) + tt if start_pos is not None else used[:, None].long() - tq + tt
+                q = headdim.rotate(q, rope[0].float(), rope[1].float(), pos)
+            q = headdim.pad(q, k_cache.shape[-1])
+            kw = {"softmax_scale": 1.0 / math.sqrt(d)}
         if tq == 1 and base_attn_mask is None:
             # One new token: the bottom-right causal mask admits every cached
             # key, so causal and non-causal coincide (mint/nn/flashattn.py:245-264).
-            return ops.attention_decode(q, k_cache, v_cache, used, window_left=window_left,
-                                        alibi_slopes=alibi_slopes, **kw)
+            o = ops.attention_decode(q, k_cache, v_cache, used, window_left=window_left,
+                                     alibi_slopes=alibi_slopes, **kw)
+            return o if native else o[..., :d]
         # Chunked prefill over the cache: the launch covers the keys the cache
         # can hold now (its host-side length bound), not max_seq_len.
         lk = kv_cache.max_seq_len if kv_cache.len_bound is None else max(1, kv_cache.len_bound)
         if base_attn_mask is not None:
             kw["attn_mask"] = base_attn_mask
-        return ops.attention_prefill(q, k_cache[:b, :lk], v_cache[:b, :lk], causal=causal, window_left=window_left,
-                                     alibi_slopes=alibi_slopes, seqused_k=used, **kw)
+        o = ops.attention_prefill(q, k_cache[:b, :lk], v_cache[:b, :lk], causal=causal, window_left=window_left,
+                                  alibi_slopes=alibi_slopes, seqused_k=used, **kw)
+        return o if native else o[..., :d]
 
 
 def _needs_grad(*ts) -> bool:

@@ -130,3 +130,23 @@ def test_kvcache_host_bound_rejects_overflow_before_any_launch():
     assert kv.len_bound is None
     kv.reset()
     assert kv.len_bound == 0
+
+
+def test_head_dim_padding_helpers():
+    """goda_amd.headdim: the padded size, zero padding, and the torch RoPE
+    used for head dims without kernels (against the oracle's rotation)."""
+    from goda_amd import headdim
+
+    assert [headdim.padded(d) for d in (8, 32, 64, 80, 96, 128, 160, 256)] == [64, 64, 64, 128, 128, 128, 256, 256]
+    with pytest.raises(ValueError):
+        headdim.padded(320)
+    x = torch.randn(2, 5, 3, 96)
+    xp = headdim.pad(x, 128)
+    assert xp.shape[-1] == 128 and torch.equal(xp[..., :96], x) and torch.all(xp[..., 96:] == 0)
+    cos, sin = ref.rope_tables(40, 96, 10000.0)
+    pos = torch.arange(7, 12)
+    assert torch.allclose(headdim.rotate(x, cos, sin, pos), ref.apply_rope(x, cos, sin, pos), atol=1e-6)
+    # per-sequence positions [B, T]
+    pb = torch.stack([pos, pos + 3])
+    r = headdim.rotate(x, cos, sin, pb)
+    assert torch.allclose(r[1], ref.apply_rope(x[1:2], cos, sin, pos + 3)[0], atol=1e-6)
