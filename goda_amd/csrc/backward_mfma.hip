@@ -481,7 +481,9 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         int lo_lim = -1, hi_lim = g.lq - 1 - rel;
         if (a.causal) lo_lim = key - diag - rel;
         if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
-        const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27;
+        // Visible rows as one bit per register offset (bit off = 8 gq + e).
+        uint32_t vis = key_ok ? range_bits(lo_lim, hi_lim) : 0u;
+        if (MASK) vis &= mword;
         const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
         float pr[16], ds[16];
 #pragma unroll
@@ -491,14 +493,21 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * gq + e;
-            const int off = 8 * gq + e;
             float t = s[r] * c;
-            if (ALIBI) t += base - slope2 * (float)off;
-            float pv = fast_exp2(t - l2[e]);
-            if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
-            if (MASK) pv = keep_if_bit(pv, mword, off, 0.f);
-            pr[r] = pv;
-            ds[r] = pv * (dp[r] - dl[e]);
+            if (ALIBI) t += base - slope2 * (float)(8 * gq + e);
+            pr[r] = fast_exp2(t - l2[e]);
+            ds[r] = pr[r] * (dp[r] - dl[e]);
+          }
+        }
+        // Hidden entries are replaced (not scaled: exp2 of a hidden score
+        // may overflow) on the tiles where some lane of the wave has one; a
+        // wave-uniform branch, most tiles skip it.
+        if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 8 * (r >> 2) + (r & 3);
+            pr[r] = keep_if_bit(pr[r], vis, off, 0.f);
+            ds[r] = keep_if_bit(ds[r], vis, off, 0.f);
           }
         }
         xchg(it, 0) = pack8<v8, T>(pr);
@@ -720,7 +729,10 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     if (a.causal) lo_lim = key - diag - rel;
     if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
     const bool key_ok = key < g.lk;
-    const bool need_mask = !key_ok || lo_lim > 0 || hi_lim < 27;
+    // visible rows as bits; hidden entries replaced on the tiles that have
+    // some (as in the 8-wave kernel)
+    uint32_t vis = key_ok ? range_bits(lo_lim, hi_lim) : 0u;
+    if (MASK) vis &= mword;
     const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
     float pr[16], ds[16];
 #pragma unroll
@@ -730,14 +742,18 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * gq + e;
-        const int off = 8 * gq + e;
         float t = s[r] * c;
-        if (ALIBI) t += base - slope2 * (float)off;
-        float pv = fast_exp2(t - l2[e]);
-        if (need_mask) pv = (key_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
-        if (MASK) pv = keep_if_bit(pv, mword, off, 0.f);
-        pr[r] = pv;
-        ds[r] = pv * (dp[r] - dl[e]);
+        if (ALIBI) t += base - slope2 * (float)(8 * gq + e);
+        pr[r] = fast_exp2(t - l2[e]);
+        ds[r] = pr[r] * (dp[r] - dl[e]);
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int off = 8 * (r >> 2) + (r & 3);
+        pr[r] = keep_if_bit(pr[r], vis, off, 0.f);
+        ds[r] = keep_if_bit(ds[r], vis, off, 0.f);
       }
     }
     store_next(1);
@@ -982,25 +998,27 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     if (a.causal) hi_lim = min(hi_lim, iabs - rel);
     const int lo_lim = use_window ? iabs - a.window_left - rel : 0;
     const bool row_ok = i < g.lq;
-    const bool need_mask = !row_ok || hi_lim < kBKV - 1 || lo_lim > 0;
+    // Visible keys as bits (bit off; one key tile is 32 keys); hidden
+    // entries are replaced (exp2 of a hidden score may overflow) on the
+    // tiles where some lane of the wave has one, a wave-uniform branch.
+    static_assert(MT == 1, "one 32-bit visibility word per key tile");
+    uint32_t vis = row_ok ? range_bits(lo_lim, hi_lim) : 0u;
+    if (MASK) vis &= mword;
     const float base = ALIBI ? slope2 * (float)(rel - iabs) : 0.f;
-    v8 dsf[KS2];
+    float ds[16];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float ds[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int off = 32 * mt + 8 * (r >> 2) + (r & 3);
-        float t = s[mt][r] * c;
-        if (ALIBI) t += base + slope2 * (float)off;
-        float pv = fast_exp2(t - l2);
-        if (need_mask) pv = (row_ok && off >= lo_lim && off <= hi_lim) ? pv : 0.f;
-        if (MASK) pv = keep_if_bit(pv, mword, off, 0.f);
-        ds[r] = pv * (dp[mt][r] - dl);
-      }
-      dsf[2 * mt] = pack8<v8, T>(ds);
-      dsf[2 * mt + 1] = pack8<v8, T>(ds + 8);
+    for (int r = 0; r < 16; ++r) {
+      float t = s[0][r] * c;
+      if (ALIBI) t += base + slope2 * (float)(8 * (r >> 2) + (r & 3));
+      ds[r] = fast_exp2(t - l2) * (dp[0][r] - dl);
     }
+    if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ds[r] = keep_if_bit(ds[r], vis, 8 * (r >> 2) + (r & 3), 0.f);
+    }
+    v8 dsf[KS2];
+    dsf[0] = pack8<v8, T>(ds);
+    dsf[1] = pack8<v8, T>(ds + 8);
     // dQ^T += K^T dS^T
 #pragma unroll
     for (int ks2 = 0; ks2 < KS2; ++ks2)
