@@ -90,6 +90,19 @@ __device__ __forceinline__ int64_t kv_tile_index(int b, int j, int hk, int ntk, 
   return ((int64_t)b * ntk + j) * heads_kv + hk;
 }
 
+// Step it = h * nq + q of a walk over (query head h of a KV group, query
+// tile q of nq), advanced one step at a time: no division per tile.
+struct QWalk {
+  int h, q, nq;
+  __device__ __forceinline__ QWalk(int it, int nq_) : h(nq_ > 0 ? it / nq_ : 0), q(it - h * nq_), nq(nq_) {}
+  __device__ __forceinline__ void next() {
+    if (++q == nq) {
+      q = 0;
+      ++h;
+    }
+  }
+};
+
 template <typename T>
 __device__ __forceinline__ const T* grow(const void* base, int64_t sb, int64_t st, int64_t sh, bool varlen, int b,
                                          int64_t row, int h) {
@@ -411,13 +424,14 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
 
   v8 stg[LOADS];
   v8 stg_stat;
-  auto tile_load = [&](int it) {
-    const int hq = hk * p.group + it / nq;
-    const int qt = qt_lo + it % nq;
-    const v8* src = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
+  QWalk ld(0, nq);  // the next tile to load; loads come in walk order
+  auto tile_load = [&]() {
+    const int64_t t = q_tile_index(b, qt_lo + ld.q, hk * p.group + ld.h, p.ntq, a.heads_q);
+    const v8* src = reinterpret_cast<const v8*>(p.qimg + t * QI::BYTES);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) stg[i] = src[tid + i * kWavesKv * 64];
     if (tid < QI::STAT_CH) stg_stat = src[QI::STAT + tid];
+    ld.next();
   };
   auto tile_store = [&](int it) {
     v8* dst = reinterpret_cast<v8*>(smem + (it % kKvStages) * QI::BYTES);
@@ -427,11 +441,22 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   };
   auto stage = [&](int it) { return reinterpret_cast<const v8*>(smem + (it % kKvStages) * QI::BYTES); };
   auto xchg = [&](int it, int c) -> v8& { return xbuf[(((it & 1) * 4 + pair) * 4 + c) * 64 + lane]; };
-
-  if (n > 0) {
-    tile_load(0);
-    tile_store(0);
-  }
+  // Iterations 0..n of a role (B runs one tile behind A, so both take n + 1
+  // barriers). `pre(it)` issues the role's own global loads ahead of the
+  // tile loads (the load counter drains in order).
+  auto walk = [&](auto&& pre, auto&& step) {
+    if (n > 0) {
+      tile_load();
+      tile_store(0);
+    }
+    for (int it = 0; it <= n; ++it) {
+      ring_barrier();
+      pre(it);
+      if (it + 1 < n) tile_load();
+      step(it);
+      if (it + 1 < n) tile_store(it + 1);
+    }
+  };
 
   if (!role_b) {
     // ---- A: scores --------------------------------------------------------
@@ -454,18 +479,21 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
     }
     const float c = p.scale_log2;
     const bool key_ok = key < g.lk;
-    for (int it = 0; it <= n; ++it) {
-      ring_barrier();
-      if (it + 1 < n) tile_load(it + 1);
+    QWalk cu(0, nq);
+    uint32_t mword = 0;
+    auto pre = [&](int it) {
+      // the caller's mask bits of this key for the tile's 32 rows
+      if (MASK && key_ok && it < n)
+        mword = p.mask_t[b * p.mt_stride_b + (hk * p.group + cu.h) * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo +
+                         cu.q] >> (4 * hi);
+    };
+    walk(pre, [&](int it) {
       if (it < n) {
-        const int hq = hk * p.group + it / nq;
-        const int q0 = (qt_lo + it % nq) * kQRows;
+        const int hq = hk * p.group + cu.h;
+        const int q0 = (qt_lo + cu.q) * kQRows;
+        cu.next();
         const v8* st = stage(it);
         const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
-        // The caller's mask bits of this key for the tile's 32 rows.
-        uint32_t mword = 0;
-        if (MASK && key_ok)
-          mword = p.mask_t[b * p.mt_stride_b + hq * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo + it % nq] >> (4 * hi);
         // S [rows][keys] and dP: two interleaved accumulation chains.
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -515,8 +543,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         xchg(it, 2) = pack8<v8, T>(ds);
         xchg(it, 3) = pack8<v8, T>(ds + 8);
       }
-      if (it + 1 < n) tile_store(it + 1);
-    }
+    });
     return;
   }
 
@@ -524,9 +551,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   f32x16 dv[MD], dk[MD];
 #pragma unroll
   for (int md = 0; md < MD; ++md) dv[md] = dk[md] = f32x16{};
-  for (int it = 0; it <= n; ++it) {
-    ring_barrier();
-    if (it + 1 < n) tile_load(it + 1);
+  walk([](int) {}, [&](int it) {
     if (it > 0) {
       const v8* st = stage(it - 1);
       const v8 p0 = xchg(it - 1, 0), p1 = xchg(it - 1, 1);
@@ -543,8 +568,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       }
       lead_schedule<T, 4 * MD, 4>();
     }
-    if (it + 1 < n) tile_store(it + 1);
-  }
+  });
 
   // ---- epilogue: lane l32 owns key row `key`; register (md, r) is head-dim
   // 32 md + 8 (r/4) + 4 hi + r%4.
@@ -663,13 +687,11 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
 
   v8 stg[PART];
   v8 stg_stat;
-  auto src_of = [&](int it) {
-    const int hq = hk * p.group + it / nq;
-    const int qt = qt_lo + it % nq;
-    return reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
+  auto src_of = [&](const QWalk& w) {
+    const int64_t t = q_tile_index(b, qt_lo + w.q, hk * p.group + w.h, p.ntq, a.heads_q);
+    return reinterpret_cast<const v8*>(p.qimg + t * QI::BYTES);
   };
-  auto load_part = [&](int it, int part) {
-    const v8* src = src_of(it);
+  auto load_part = [&](const v8* src, int part) {
 #pragma unroll
     for (int i = 0; i < PART; ++i) stg[i] = src[tid + (part * PART + i) * NTH];
     if (part == 0 && tid < QI::STAT_CH) stg_stat = src[QI::STAT + tid];
@@ -682,10 +704,12 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
   };
 
   const float c = p.scale_log2;
+  QWalk cu(it0, nq), nw(it0, nq);
   if (it0 < it1) {
+    const v8* src = src_of(cu);
 #pragma unroll
     for (int part = 0; part < kWideParts; ++part) {
-      load_part(it0, part);
+      load_part(src, part);
       store_part(it0, part);
     }
   }
@@ -693,9 +717,12 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
   for (int it = it0; it < it1; ++it) {
     // The next tile is staged into the other stage (on the last tile: this
     // tile again, into a stage nobody reads), so the loop body is branch-free.
-    const int nx = it + 1 < it1 ? it + 1 : it;
-    const int hq = hk * p.group + it / nq;
-    const int q0 = (qt_lo + it % nq) * kQRows;
+    if (it + 1 < it1) nw.next();
+    const v8* nsrc = src_of(nw);
+    const int hq = hk * p.group + cu.h;
+    const int qt = qt_lo + cu.q;
+    const int q0 = qt * kQRows;
+    cu.next();
     const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
     const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
     const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
@@ -706,11 +733,11 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
     };
 
-    load_part(nx, 0);
+    load_part(nsrc, 0);
     // The caller's mask bits of this key for the tile's 32 rows.
     uint32_t mword = 0;
     if (MASK && key < g.lk)
-      mword = p.mask_t[b * p.mt_stride_b + hq * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo + it % nq] >> (4 * hi);
+      mword = p.mask_t[b * p.mt_stride_b + hq * p.mt_stride_h + (int64_t)key * p.ntq + qt] >> (4 * hi);
     // S and dP: two independent accumulation chains, interleaved.
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -720,7 +747,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     }
     lead_schedule<T, 2 * KS, 4>();
     store_next(0);
-    load_part(nx, 1);
+    load_part(nsrc, 1);
 
     // P and dS; visibility as a range of the register's row offset
     // off = row - (q0 + 4 hi).
@@ -757,7 +784,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       }
     }
     store_next(1);
-    load_part(nx, 2);
+    load_part(nsrc, 2);
     const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
@@ -766,7 +793,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     }
     lead_schedule<T, 2 * MD, 4>();
     store_next(2);
-    load_part(nx, 3);
+    load_part(nsrc, 3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {

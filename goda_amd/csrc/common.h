@@ -179,13 +179,11 @@ __device__ __forceinline__ const uint32_t* mask_row(const goda_prefill_args& a, 
 __device__ __forceinline__ bool mask_bit(const uint32_t* row, int j) { return (row[j >> 5] >> (j & 31)) & 1u; }
 
 // Bits lo..hi of a 32-bit word (0 when lo > hi; lo and hi may lie outside
-// 0..31 and are clamped).
+// 0..31). Branch-free: 64-bit shifts by 0..32.
 __device__ __forceinline__ uint32_t range_bits(int lo, int hi) {
-  lo = max(lo, 0);
-  hi = min(hi, 31);
-  if (lo > hi) return 0u;
-  const uint32_t upto = hi == 31 ? ~0u : (1u << (hi + 1)) - 1u;
-  return upto & ~((1u << lo) - 1u);
+  const int l = min(max(lo, 0), 32);
+  const int h = min(max(hi, -1), 31) + 1;
+  return (uint32_t)(~0ull << l) & ~(uint32_t)(~0ull << h);
 }
 
 // Keep `x` where the 1-bit field `bit` of `w` is set, else `repl`: one
