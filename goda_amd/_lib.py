@@ -17,7 +17,7 @@ from pathlib import Path
 _LIB_ENV = "GODA_ATTN_LIB"
 _DEFAULT = Path(__file__).resolve().parent / "lib" / "libgoda_attn.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -195,6 +195,8 @@ class PrefillGrads(ctypes.Structure):
         ("dv_stride_b", _i64),
         ("dv_stride_t", _i64),
         ("dv_stride_h", _i64),
+        ("dq_norm_weight", _vp),
+        ("dk_norm_weight", _vp),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
         ("timing_begin", _vp),

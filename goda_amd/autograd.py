@@ -1,12 +1,14 @@
 """Differentiable prefill attention on the HIP kernels.
 
 `attention_prefill(q, k, v, **options)` takes the options of
-`ops.attention_prefill` and returns o; when grad mode is on and q, k or v
-requires grad it runs through `PrefillAttention`, whose backward calls
-`goda_attn_prefill_bwd` with the forward's saved o and lse (the structure of
-FlashAttentionGQAKernel.backward, kernels_/flash_attn_gqa/cuda.py:577-658).
-Tensors among the options (RoPE tables, ALiBi slopes, cu_seqlens, the
-boolean mask) are treated as constants.
+`ops.attention_prefill` and returns o; when grad mode is on and q, k, v or a
+fused QK-RMSNorm weight requires grad it runs through `PrefillAttention`,
+whose backward calls `goda_attn_prefill_bwd` with the forward's saved o and
+lse (the structure of FlashAttentionGQAKernel.backward,
+kernels_/flash_attn_gqa/cuda.py:577-658). The norm weights
+(`q_norm_weight`, `k_norm_weight`) get their gradients from the same call;
+the other tensors among the options (RoPE tables, ALiBi slopes, cu_seqlens,
+the boolean mask) are treated as constants.
 """
 
 from __future__ import annotations
@@ -20,17 +22,29 @@ from . import headdim, ops
 
 class PrefillAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, options: dict):
-        o, lse = ops.attention_prefill(q, k, v, return_lse=True, **options)
+    def forward(ctx, q, k, v, q_norm_weight, k_norm_weight, options: dict):
+        opts = dict(options)
+        if q_norm_weight is not None:
+            opts["q_norm_weight"] = q_norm_weight
+        if k_norm_weight is not None:
+            opts["k_norm_weight"] = k_norm_weight
+        o, lse = ops.attention_prefill(q, k, v, return_lse=True, **opts)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.options = options
+        ctx.options = opts
+        ctx.norm_dtypes = (None if q_norm_weight is None else q_norm_weight.dtype,
+                           None if k_norm_weight is None else k_norm_weight.dtype)
         return o
 
     @staticmethod
     def backward(ctx, d_o):
         q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = ops.attention_prefill_bwd(q, k, v, o, lse, d_o, **ctx.options)
-        return dq, dk, dv, None
+        grads = ops.attention_prefill_bwd(q, k, v, o, lse, d_o, **ctx.options)
+        if len(grads) == 3:
+            return (*grads, None, None, None)
+        dq, dk, dv, dqn, dkn = grads
+        dqn = None if dqn is None else dqn.to(ctx.norm_dtypes[0])
+        dkn = None if dkn is None else dkn.to(ctx.norm_dtypes[1])
+        return dq, dk, dv, dqn, dkn, None
 
 
 def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **options) -> torch.Tensor:
@@ -40,9 +54,14 @@ def attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **optio
     if m is not None and not isinstance(m, ops.PackedMask) and q.dim() == 4:
         # Packed once, shared by the forward and the backward.
         options["attn_mask"] = ops.pack_mask(m, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.device)
-    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+    qn, kn = options.get("q_norm_weight"), options.get("k_norm_weight")
+    wants = [t for t in (q, k, v, qn, kn) if t is not None]
+    if torch.is_grad_enabled() and any(t.requires_grad for t in wants):
+        options = dict(options)
         options.pop("return_lse", None)
-        return PrefillAttention.apply(q, k, v, options)
+        options.pop("q_norm_weight", None)
+        options.pop("k_norm_weight", None)
+        return PrefillAttention.apply(q, k, v, qn, kn, options)
     return ops.attention_prefill(q, k, v, **options)
 
 

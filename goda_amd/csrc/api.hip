@@ -194,8 +194,6 @@ int32_t goda_attn_prefill_bwd(const goda_prefill_args* a, const goda_prefill_gra
   const int32_t st = check_prefill(a, false);
   if (st != GODA_OK) return st;
   if (!g) return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: grads is NULL");
-  if (a->q_norm_weight || a->k_norm_weight)
-    return fail(GODA_ERR_UNSUPPORTED, "prefill_bwd: the fused QK-RMSNorm is forward only (keep the norm outside for training)");
   if (a->batch == 0 || (a->seqlen_q == 0 && a->seqlen_k == 0)) return ok();
   if (!a->q || !a->k || !a->v || !a->o || !g->d_o || !g->dq || !g->dk || !g->dv)
     return fail(GODA_ERR_INVALID_ARG, "prefill_bwd: NULL tensor pointer");

@@ -442,23 +442,90 @@ hipError_t launch_generic_t(const BwdParams& p, hipStream_t s) {
 
 }  // namespace
 
-int64_t prefill_bwd_workspace_bytes(const goda_prefill_args& a) {
-  if (prefill_bwd_mfma_supported(a)) return prefill_bwd_mfma_workspace_bytes(a);
-  return (int64_t)a.heads_q * a.batch * a.seqlen_q * (int64_t)sizeof(float);
+namespace {
+
+int64_t align_up(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace layout: the kernels' own region, then with the fused QK-RMSNorm
+// the dw partials and, for the generic kernels (which read q / k rows
+// themselves), the normalized q and k rows.
+struct BwdLayout {
+  int64_t norm_part = 0, q_rows = 0, k_rows = 0, bytes = 0;
+};
+
+BwdLayout bwd_layout(const goda_prefill_args& a) {
+  BwdLayout l;
+  const bool mf = prefill_bwd_mfma_supported(a);
+  l.bytes = mf ? prefill_bwd_mfma_workspace_bytes(a) : (int64_t)a.heads_q * a.batch * a.seqlen_q * (int64_t)sizeof(float);
+  if (!a.q_norm_weight && !a.k_norm_weight) return l;
+  l.norm_part = align_up(l.bytes);
+  l.bytes = l.norm_part + norm_bwd_part_bytes(a);
+  if (!mf) {
+    const int64_t es = a.dtype == GODA_DTYPE_F32 ? 4 : 2;
+    if (a.q_norm_weight) {
+      l.q_rows = align_up(l.bytes);
+      l.bytes = l.q_rows + (int64_t)a.batch * a.seqlen_q * a.heads_q * a.head_dim * es;
+    }
+    if (a.k_norm_weight) {
+      l.k_rows = align_up(l.bytes);
+      l.bytes = l.k_rows + (int64_t)a.batch * a.seqlen_k * a.heads_kv * a.head_dim * es;
+    }
+  }
+  return l;
 }
 
-hipError_t launch_prefill_bwd(const BwdParams& p, hipStream_t s) {
-  if (prefill_bwd_mfma_supported(p.a)) return launch_prefill_bwd_mfma(p, s);
-  switch (p.a.dtype) {
-    case GODA_DTYPE_F32:
-      return launch_generic_t<float>(p, s);
-    case GODA_DTYPE_F16:
-      return launch_generic_t<f16>(p, s);
-    case GODA_DTYPE_BF16:
-      return launch_generic_t<bf16>(p, s);
-    default:
-      return hipErrorNotSupported;
+}  // namespace
+
+int64_t prefill_bwd_workspace_bytes(const goda_prefill_args& a) { return bwd_layout(a).bytes; }
+
+hipError_t launch_prefill_bwd(const BwdParams& p0, hipStream_t s) {
+  const goda_prefill_args& a = p0.a;
+  const bool norm = a.q_norm_weight || a.k_norm_weight;
+  const bool mf = prefill_bwd_mfma_supported(a);
+  const BwdLayout l = bwd_layout(a);
+  unsigned char* ws = reinterpret_cast<unsigned char*>(p0.g.workspace);
+  BwdParams p = p0;
+  hipError_t e;
+  if (norm && !mf) {
+    // The generic kernels read q / k rows themselves: hand them the
+    // normalized rows (RoPE stays theirs), so dq / dk come out as the
+    // gradients of those rows, as on the MFMA path.
+    if (a.q_norm_weight) {
+      if ((e = launch_norm_rows(a, true, ws + l.q_rows, s)) != hipSuccess) return e;
+      p.a.q = ws + l.q_rows;
+      p.a.q_stride_h = a.head_dim;
+      p.a.q_stride_t = (int64_t)a.heads_q * a.head_dim;
+      p.a.q_stride_b = (int64_t)a.seqlen_q * p.a.q_stride_t;
+    }
+    if (a.k_norm_weight) {
+      if ((e = launch_norm_rows(a, false, ws + l.k_rows, s)) != hipSuccess) return e;
+      p.a.k = ws + l.k_rows;
+      p.a.k_stride_h = a.head_dim;
+      p.a.k_stride_t = (int64_t)a.heads_kv * a.head_dim;
+      p.a.k_stride_b = (int64_t)a.seqlen_k * p.a.k_stride_t;
+    }
+    p.a.q_norm_weight = p.a.k_norm_weight = nullptr;
   }
+  if (mf) {
+    e = launch_prefill_bwd_mfma(p, s);
+  } else {
+    switch (a.dtype) {
+      case GODA_DTYPE_F32:
+        e = launch_generic_t<float>(p, s);
+        break;
+      case GODA_DTYPE_F16:
+        e = launch_generic_t<f16>(p, s);
+        break;
+      case GODA_DTYPE_BF16:
+        e = launch_generic_t<bf16>(p, s);
+        break;
+      default:
+        e = hipErrorNotSupported;
+    }
+  }
+  if (e != hipSuccess || !norm) return e;
+  // dx and dw from the caller's rows (p0.a: the un-normalized q, k).
+  return launch_norm_bwd(a, p0.g, reinterpret_cast<float*>(ws + l.norm_part), s);
 }
 
 }  // namespace goda

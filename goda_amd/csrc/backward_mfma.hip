@@ -109,6 +109,48 @@ __device__ __forceinline__ const T* grow(const void* base, int64_t sb, int64_t s
   return reinterpret_cast<const T*>(base) + (varlen ? 0 : (int64_t)b * sb) + row * st + (int64_t)h * sh;
 }
 
+// Elements c..c+7 and c+D/2..c+D/2+7 of a q or k row, held by one of the
+// row's N consecutive lanes: goda's RMSNorm (weight w, or none) and then the
+// half-split rotation at `pos` (when `rot`), in fp32 and rounded once, as
+// the forward's pre-passes compute them. Every lane of the row's group must
+// call it (the norm's sum of squares is a group reduction).
+template <typename T, int D, int N>
+__device__ __forceinline__ void norm_rope_row(typename Vec<T>::v8& h1, typename Vec<T>::v8& h2, int c, const float* w,
+                                              float eps, bool rot, int pos, const goda_prefill_args& a) {
+  if (!w && !rot) return;
+  float x1[8], x2[8];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x1[e] = (float)h1[e];
+    x2[e] = (float)h2[e];
+    ss = fmaf(x1[e], x1[e], fmaf(x2[e], x2[e], ss));
+  }
+  if (w) {
+    const float inv = rms_scale(lane_group_sum<N>(ss), D, eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x1[e] *= inv * (1.f + w[c + e]);
+      x2[e] *= inv * (1.f + w[c + D / 2 + e]);
+    }
+  }
+  if (rot) {
+    const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
+    const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y1 = x1[e] * cs[e] - x2[e] * sn[e];
+      x2[e] = x1[e] * sn[e] + x2[e] * cs[e];
+      x1[e] = y1;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    h1[e] = (T)x1[e];
+    h2[e] = (T)x2[e];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 1. query-side images
 // ---------------------------------------------------------------------------
@@ -128,7 +170,8 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
   const int tid = threadIdx.x;
   constexpr int HALF8 = D / 16;
 
-  // rotated q and dO rows (zero past the sequence)
+  // normalized, rotated q and dO rows (zero past the sequence); a row's
+  // HALF8 threads are consecutive lanes (and the loop is uniform per wave)
   for (int idx = tid; idx < kQRows * HALF8; idx += 256) {
     const int r = idx / HALF8;
     const int c = (idx % HALF8) * 8;
@@ -141,18 +184,9 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
       q2 = ld_vec<v8>(qr + c + D / 2);
       g1 = ld_vec<v8>(gr + c);
       g2 = ld_vec<v8>(gr + c + D / 2);
-      if (a.rope_q) {
-        const int pos = rope_qpos(a, diag, i);
-        const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
-        const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x1 = (float)q1[e], x2 = (float)q2[e];
-          q1[e] = (T)(x1 * cs[e] - x2 * sn[e]);
-          q2[e] = (T)(x1 * sn[e] + x2 * cs[e]);
-        }
-      }
     }
+    norm_rope_row<T, D, HALF8>(q1, q2, c, a.q_norm_weight, a.norm_eps, i < g.lq && a.rope_q,
+                               i < g.lq ? rope_qpos(a, diag, i) : 0, a);
     st_vec<v8>(&qrows[r][c], q1);
     st_vec<v8>(&qrows[r][c + D / 2], q2);
     st_vec<v8>(&grows[r][c], g1);
@@ -244,18 +278,9 @@ __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
       k2 = ld_vec<v8>(kr + c + D / 2);
       v1 = ld_vec<v8>(vr + c);
       v2 = ld_vec<v8>(vr + c + D / 2);
-      if (a.rope_k) {
-        const int pos = a.rope_k_offset + row;
-        const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
-        const float* sn = a.rope_sin + (int64_t)pos * (D / 2) + c;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x1 = (float)k1[e], x2 = (float)k2[e];
-          k1[e] = (T)(x1 * cs[e] - x2 * sn[e]);
-          k2[e] = (T)(x1 * sn[e] + x2 * cs[e]);
-        }
-      }
     }
+    norm_rope_row<T, D, HALF8>(k1, k2, c, a.k_norm_weight, a.norm_eps, row < g.lk && a.rope_k, a.rope_k_offset + row,
+                               a);
     st_vec<v8>(&krows[r][c], k1);
     st_vec<v8>(&krows[r][c + D / 2], k2);
     st_vec<v8>(&vrows[r][c], v1);

@@ -91,6 +91,14 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
+// Sum over aligned groups of N consecutive lanes (N a power of two <= 64).
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < N; m <<= 1) v += shfl_xor_f(v, m);
+  return v;
+}
+
 // 16-byte and 8-byte vector memory helpers on raw element pointers.
 template <typename V, typename T>
 __device__ __forceinline__ V ld_vec(const T* p) {

@@ -60,6 +60,13 @@ struct BwdParams {
 int64_t prefill_bwd_workspace_bytes(const goda_prefill_args& a);
 hipError_t launch_prefill_bwd(const BwdParams& p, hipStream_t s);
 bool prefill_bwd_mfma_supported(const goda_prefill_args& a);
+// Fused QK-RMSNorm backward (norm_bwd.hip): fp32 dw partials' bytes, the
+// normalized rows of q or k (contiguous [batch, seqlen, heads, head_dim],
+// packed rows at their packed index) for the generic kernels, and dx / dw
+// from the attention backward's dq / dk (gradients of the normalized rows).
+int64_t norm_bwd_part_bytes(const goda_prefill_args& a);
+hipError_t launch_norm_rows(const goda_prefill_args& a, bool q_side, void* dst, hipStream_t s);
+hipError_t launch_norm_bwd(const goda_prefill_args& a, const goda_prefill_grads& g, float* part, hipStream_t s);
 int64_t prefill_bwd_mfma_workspace_bytes(const goda_prefill_args& a);
 hipError_t launch_prefill_bwd_mfma(BwdParams p, hipStream_t s);
 

@@ -1,0 +1,233 @@
+// Backward of the fused QK-RMSNorm (goda's RMSNorm, mint/nn/norm.py:17-27,
+// applied to every q and k head row before RoPE, mint/nn/attn.py:57-60):
+//   y = x r g,  r = rsqrt(mean(x^2) + eps),  g = 1 + w   (fp32),
+//   dx = r (g dy - x^ mean(x^ g dy)),  x^ = x r,  dw = sum over rows of x^ dy.
+// The attention backward leaves dy (the gradient of the normalized, unrotated
+// rows, in the caller's dq / dk buffer and dtype, as the unfused path holds
+// it); norm_bwd_kernel turns it into dx in place and writes one fp32 partial
+// of dw per workgroup; norm_dw_reduce_kernel sums the partials in a fixed
+// order (no atomics: the result does not depend on scheduling).
+// norm_rows_kernel writes the normalized rows themselves, for the backward
+// kernels that read q / k rows directly instead of through the MFMA path's
+// operand images.
+//
+// Row layout: a group of D/8 lanes holds one row, 8 elements per lane
+// (16-byte loads at 16-bit dtypes); a wave covers 512/D rows at a time and a
+// workgroup of 4 waves kNormRows rows of one (sequence, head).
+
+#include "common.h"
+#include "launch.h"
+#include "mfma_common.h"
+
+namespace goda {
+namespace {
+
+constexpr int kNormRows = 256;  // rows per workgroup
+
+template <typename T, int D>
+struct NormGeom {
+  static constexpr int LPR = D / 8;        // lanes per row
+  static constexpr int RPW = 64 / LPR;     // rows per wave step
+  static constexpr int SLOTS = 4 * RPW;    // row groups of a workgroup
+};
+
+struct NormRows {
+  const void* x;  // rows to normalize (the caller's q or k)
+  int64_t x_sb, x_st, x_sh;
+  void* y;        // norm_rows: normalized rows; norm_bwd: dy in, dx out
+  int64_t y_sb, y_st, y_sh;
+  const float* w;
+  float eps;
+  float* part;    // norm_bwd: fp32 [gridDim.z][gridDim.y][gridDim.x][D]
+  int heads;
+  bool q_side;    // rows of q (lengths lq) or of k (lengths lk)
+};
+
+__device__ __forceinline__ int norm_len(const goda_prefill_args& a, int b, bool q_side, int64_t* row0) {
+  const SeqGeom g = seq_geom(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k);
+  *row0 = q_side ? g.q_row0 : g.k_row0;
+  if (q_side) return g.lq;
+  // padded batches: the rows past seqused_k are zero in dk and stay zero
+  return g.lk;
+}
+
+template <typename T, int D, bool BWD>
+__global__ void __launch_bounds__(256) norm_rows_kernel(const goda_prefill_args a, const NormRows n) {
+  typedef typename Vec<T>::v8 v8;
+  typedef NormGeom<T, D> NG;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane / NG::LPR, c = (lane % NG::LPR) * 8;
+  int64_t row0;
+  const int len = norm_len(a, b, n.q_side, &row0);
+  const bool varlen = (n.q_side ? a.cu_seqlens_q : a.cu_seqlens_k) != nullptr;
+  float g[8], acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    g[e] = 1.f + n.w[c + e];
+    acc[e] = 0.f;
+  }
+  const int first = blockIdx.x * kNormRows;
+  // The row loop is uniform over the workgroup: every lane of a row group
+  // takes part in its reductions (rows past the sequence load zeros).
+  for (int r = first + wave * NG::RPW + sub; r < first + kNormRows; r += 4 * NG::RPW) {
+    const bool ok = r < len;
+    const int64_t row = row0 + r;
+    const T* xp = reinterpret_cast<const T*>(n.x) + (varlen ? 0 : (int64_t)b * n.x_sb) + row * n.x_st + (int64_t)h * n.x_sh + c;
+    T* yp = reinterpret_cast<T*>(n.y) + (varlen ? 0 : (int64_t)b * n.y_sb) + row * n.y_st + (int64_t)h * n.y_sh + c;
+    v8 xv = {};
+    if (ok) xv = ld_vec<v8>(xp);
+    float x[8];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = (float)xv[e];
+      ss = fmaf(x[e], x[e], ss);
+    }
+    const float rs = rms_scale(lane_group_sum<NG::LPR>(ss), D, n.eps);
+    if (!BWD) {
+      v8 out;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = (T)(x[e] * rs * g[e]);
+      if (ok) st_vec<v8>(yp, out);
+      continue;
+    }
+    v8 dv = {};
+    if (ok) dv = ld_vec<v8>(yp);
+    float dy[8], t = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      dy[e] = (float)dv[e];
+      x[e] *= rs;  // x^
+      t = fmaf(x[e] * g[e], dy[e], t);
+      acc[e] = fmaf(x[e], dy[e], acc[e]);
+    }
+    const float m = lane_group_sum<NG::LPR>(t) / (float)D;
+    v8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (T)(rs * (g[e] * dy[e] - x[e] * m));
+    if (ok) st_vec<v8>(yp, out);
+  }
+  if (!BWD) return;
+  // dw partial of this workgroup: row groups in slots, summed in slot order.
+  __shared__ float sdw[NG::SLOTS][D];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sdw[wave * NG::RPW + sub][c + e] = acc[e];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float s = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < NG::SLOTS; ++k) s += sdw[k][d];
+    const int64_t blk = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    n.part[blk * D + d] = s;
+  }
+}
+
+__global__ void __launch_bounds__(256) norm_dw_reduce_kernel(const float* part, int64_t nparts, int d_model,
+                                                             float* dw) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  if (d >= d_model) return;
+  float s = 0.f;
+  for (int64_t k = 0; k < nparts; ++k) s += part[k * d_model + d];
+  dw[d] = s;
+}
+
+template <typename T, int D>
+hipError_t launch_rows(const goda_prefill_args& a, const NormRows& n, bool bwd, int64_t seqlen, hipStream_t s) {
+  const dim3 grid((unsigned)((seqlen + kNormRows - 1) / kNormRows), (unsigned)n.heads, (unsigned)a.batch);
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return hipSuccess;
+  if (bwd)
+    norm_rows_kernel<T, D, true><<<grid, 256, 0, s>>>(a, n);
+  else
+    norm_rows_kernel<T, D, false><<<grid, 256, 0, s>>>(a, n);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_rows_t(const goda_prefill_args& a, const NormRows& n, bool bwd, int64_t seqlen, hipStream_t s) {
+  switch (a.head_dim) {
+    case 64:
+      return launch_rows<T, 64>(a, n, bwd, seqlen, s);
+    case 128:
+      return launch_rows<T, 128>(a, n, bwd, seqlen, s);
+    case 256:
+      return launch_rows<T, 256>(a, n, bwd, seqlen, s);
+    default:
+      return hipErrorNotSupported;
+  }
+}
+
+hipError_t launch_rows_any(const goda_prefill_args& a, const NormRows& n, bool bwd, int64_t seqlen, hipStream_t s) {
+  if (a.dtype == GODA_DTYPE_BF16) return launch_rows_t<bf16>(a, n, bwd, seqlen, s);
+  if (a.dtype == GODA_DTYPE_F16) return launch_rows_t<f16>(a, n, bwd, seqlen, s);
+  if (a.dtype == GODA_DTYPE_F32) return launch_rows_t<float>(a, n, bwd, seqlen, s);
+  return hipErrorNotSupported;
+}
+
+int64_t parts(int64_t seqlen, int heads, int batch) {
+  return (seqlen + kNormRows - 1) / kNormRows * heads * batch;
+}
+
+}  // namespace
+
+int64_t norm_bwd_part_bytes(const goda_prefill_args& a) {
+  int64_t n = 0;
+  if (a.q_norm_weight) n += parts(a.seqlen_q, a.heads_q, a.batch);
+  if (a.k_norm_weight) n += parts(a.seqlen_k, a.heads_kv, a.batch);
+  return n * a.head_dim * (int64_t)sizeof(float);
+}
+
+hipError_t launch_norm_rows(const goda_prefill_args& a, bool q_side, void* dst, hipStream_t s) {
+  NormRows n{};
+  const int heads = q_side ? a.heads_q : a.heads_kv;
+  const int64_t seqlen = q_side ? a.seqlen_q : a.seqlen_k;
+  n.x = q_side ? a.q : a.k;
+  n.x_sb = q_side ? a.q_stride_b : a.k_stride_b;
+  n.x_st = q_side ? a.q_stride_t : a.k_stride_t;
+  n.x_sh = q_side ? a.q_stride_h : a.k_stride_h;
+  n.y = dst;  // contiguous [batch, seqlen, heads, D] (rows of packed sequences at their packed index)
+  n.y_sh = a.head_dim;
+  n.y_st = (int64_t)heads * a.head_dim;
+  n.y_sb = seqlen * n.y_st;
+  n.w = q_side ? a.q_norm_weight : a.k_norm_weight;
+  n.eps = a.norm_eps;
+  n.heads = heads;
+  n.q_side = q_side;
+  return launch_rows_any(a, n, false, seqlen, s);
+}
+
+hipError_t launch_norm_bwd(const goda_prefill_args& a, const goda_prefill_grads& g, float* part, hipStream_t s) {
+  hipError_t e;
+  for (int side = 0; side < 2; ++side) {
+    const bool q_side = side == 0;
+    const float* w = q_side ? a.q_norm_weight : a.k_norm_weight;
+    if (!w) continue;
+    NormRows n{};
+    const int heads = q_side ? a.heads_q : a.heads_kv;
+    const int64_t seqlen = q_side ? a.seqlen_q : a.seqlen_k;
+    n.x = q_side ? a.q : a.k;
+    n.x_sb = q_side ? a.q_stride_b : a.k_stride_b;
+    n.x_st = q_side ? a.q_stride_t : a.k_stride_t;
+    n.x_sh = q_side ? a.q_stride_h : a.k_stride_h;
+    n.y = q_side ? g.dq : g.dk;
+    n.y_sb = q_side ? g.dq_stride_b : g.dk_stride_b;
+    n.y_st = q_side ? g.dq_stride_t : g.dk_stride_t;
+    n.y_sh = q_side ? g.dq_stride_h : g.dk_stride_h;
+    n.w = w;
+    n.eps = a.norm_eps;
+    n.part = part;
+    n.heads = heads;
+    n.q_side = q_side;
+    if ((e = launch_rows_any(a, n, true, seqlen, s)) != hipSuccess) return e;
+    const int64_t np = parts(seqlen, heads, a.batch);
+    float* dw = q_side ? g.dq_norm_weight : g.dk_norm_weight;
+    if (dw) {  // np == 0 writes zeros
+      norm_dw_reduce_kernel<<<(a.head_dim + 255) / 256, 256, 0, s>>>(part, np, a.head_dim, dw);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    part += np * a.head_dim;
+  }
+  return hipSuccess;
+}
+
+}  // namespace goda

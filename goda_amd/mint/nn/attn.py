@@ -81,7 +81,9 @@ class GroupedQueryAttention(nn.Module):
         fused: dict = {}
         fusable = isinstance(self.pos_embeddings, (RoPE, ALiBiPositionalBias))
         norms_plain = self.q_norm.shift is None and self.k_norm.shift is None and self.q_norm.eps == self.k_norm.eps
-        if fusable and norms_plain and not torch.is_grad_enabled():
+        # The fused norm also trains (the backward returns the weights'
+        # gradients), except over a KV cache or with doc_ids packing.
+        if fusable and norms_plain and (not torch.is_grad_enabled() or (kv_cache is None and doc_ids is None)):
             fused["qk_norm"] = (self.q_norm.scale, self.k_norm.scale, self.q_norm.eps)
         else:
             q = self.q_norm(q)

@@ -27,9 +27,10 @@ Extra keyword arguments fuse the positional encoding into the kernels:
 `rope=(cos, sin)` fp32 tables with `start_pos` (q and k are then passed
 UNROTATED), or `alibi_slopes` [Hq]; `qk_norm=(q_scale, k_scale, eps)` fuses
 goda's QK-RMSNorm (mint/nn/norm.py:17-27, weight 1 + scale, before RoPE) into
-the kernels' q/k loads when no gradient is needed (with autograd active it is
-applied as ordinary differentiable torch ops instead). There is no SDPA or
-CPU fallback.
+the kernels' q/k loads, forward and backward (the backward also returns the
+two scales' gradients); with doc_ids packing, or a differentiable call over a
+KV cache, it runs as ordinary torch ops instead. There is no SDPA or CPU
+fallback.
 """
 
 from __future__ import annotations
@@ -82,8 +83,9 @@ class FlashAttention(nn.Module):
         # Only the left window is used: the reference's SDPA path reads
         # window_size[0] alone (mint/nn/flashattn.py:251-253, 258-264).
         window_left = window_size[0] if window_size[0] >= 0 else -1
-        if qk_norm is not None and (doc_ids is not None or _needs_grad(q, k, *qk_norm[:2])):
-            # Differentiable (or pre-rotation for doc_ids packing): plain torch.
+        if qk_norm is not None and (doc_ids is not None or (kv_cache is not None and _needs_grad(q, k, *qk_norm[:2]))):
+            # doc_ids packing rotates rows before the kernel (and the norm comes
+            # before RoPE); a differentiable call over a KV cache: plain torch.
             q, k = rms_norm(q, qk_norm[0], qk_norm[2]), rms_norm(k, qk_norm[1], qk_norm[2])
             qk_norm = None
         if kv_cache is None:

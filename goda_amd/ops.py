@@ -344,9 +344,13 @@ def attention_prefill_bwd(q, k, v, o, lse, d_o, **kwargs):
     """Gradients (dq, dk, dv) of `attention_prefill` through
     `goda_attn_prefill_bwd`, from the forward's o and lse and the upstream
     gradient d_o. Takes the forward's own keyword arguments (causal, window,
-    ALiBi, RoPE, varlen, seqused_k, scale), so the scores are recomputed
-    exactly as the forward computed them. dk/dv have Hkv heads (summed over
-    each KV head's query group) and are zero for keys past seqused_k."""
+    ALiBi, RoPE, fused QK-RMSNorm, varlen, seqused_k, scale), so the scores
+    are recomputed exactly as the forward computed them. dk/dv have Hkv heads
+    (summed over each KV head's query group) and are zero for keys past
+    seqused_k. With `q_norm_weight` / `k_norm_weight` the result is
+    (dq, dk, dv, d_q_norm_weight, d_k_norm_weight): dq / dk are the gradients
+    of the rows before the norm, the weight gradients fp32 [head_dim] (None
+    for a norm not given)."""
     return plan_prefill_bwd(q, k, v, o, lse, d_o, **kwargs)()
 
 
@@ -388,6 +392,15 @@ def plan_prefill_bwd(
     g.dk_stride_b, g.dk_stride_t, g.dk_stride_h = strides(dk)
     g.dv = dv.data_ptr()
     g.dv_stride_b, g.dv_stride_t, g.dv_stride_h = strides(dv)
+    result = (dq, dk, dv)
+    norm = (kwargs.get("q_norm_weight"), kwargs.get("k_norm_weight"))
+    dw = [None, None]
+    if norm[0] is not None or norm[1] is not None:
+        for i, w in enumerate(norm):
+            if w is not None:
+                dw[i] = torch.empty(q.shape[-1], dtype=torch.float32, device=q.device)
+        g.dq_norm_weight, g.dk_norm_weight = _ptr(dw[0]), _ptr(dw[1])
+        result = (dq, dk, dv, dw[0], dw[1])
     lib = _lib.load()
     need = lib.goda_attn_prefill_bwd_workspace_size(ctypes.byref(a))
     if need < 0:
@@ -396,7 +409,7 @@ def plan_prefill_bwd(
     if need > 0:
         ws = torch.empty(int(need), dtype=torch.uint8, device=q.device)
         g.workspace, g.workspace_bytes = ws.data_ptr(), int(need)
-    return Launch("goda_attn_prefill_bwd", a, keep + (d_o, dq, dk, dv, ws), (dq, dk, dv), grads=g)
+    return Launch("goda_attn_prefill_bwd", a, keep + (d_o, dq, dk, dv, ws, *dw), result, grads=g)
 
 
 def attention_decode(*args, **kwargs):

@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define GODA_ATTN_ABI_VERSION 4
+#define GODA_ATTN_ABI_VERSION 5
 
 /* element types */
 #define GODA_DTYPE_F32 0
@@ -234,6 +234,12 @@ typedef struct goda_prefill_grads {
   int64_t dk_stride_b, dk_stride_t, dk_stride_h;
   void* dv;             /* dL/dv, like v */
   int64_t dv_stride_b, dv_stride_t, dv_stride_h;
+  /* With the fused QK-RMSNorm (fwd->q_norm_weight / k_norm_weight set), dq and
+   * dk are the gradients of the caller's rows before the norm, and these
+   * receive dL/dw of each norm weight, fp32 [head_dim] (NULL: not computed;
+   * ignored without the norm). Deterministic: no atomics. */
+  float* dq_norm_weight;
+  float* dk_norm_weight;
 
   void* workspace;      /* size from goda_attn_prefill_bwd_workspace_size */
   int64_t workspace_bytes;

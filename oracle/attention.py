@@ -402,6 +402,7 @@ def attention_grads(
     base_attn_mask: torch.Tensor | None = None,
     rope: tuple | None = None,
     scale: float | None = None,
+    qk_norm: tuple | None = None,
     dtype=torch.float32,
 ):
     """(dq, dk, dv) of `attention` for the upstream gradient d_o [B, Tq, Hq, D].
@@ -413,21 +414,31 @@ def attention_grads(
     Hkv < Hq, dk/dv of a KV head sum its query heads (SDPA's enable_gqa).
     `rope` = (cos, sin, q_positions, k_positions) rotates q and k first
     (mint/nn/pos.py:90-112, applied before attention at mint/nn/attn.py:60),
-    so dq/dk refer to the unrotated inputs. Every query row must see at least
-    one key, or come out of `attention` as 0 (then its gradients are 0).
+    so dq/dk refer to the unrotated inputs. `qk_norm` = (q_scale, k_scale,
+    eps) applies goda's QK-RMSNorm (`rms_norm`) to q and k before RoPE
+    (mint/nn/attn.py:57-60); the result is then (dq, dk, dv, d_q_scale,
+    d_k_scale), dq/dk referring to the rows before the norm. Every query row
+    must see at least one key, or come out of `attention` as 0 (then its
+    gradients are 0).
     """
     qs = q.to("cpu", dtype).detach().requires_grad_(True)
     ks = k.to("cpu", dtype).detach().requires_grad_(True)
     vs = v.to("cpu", dtype).detach().requires_grad_(True)
-    qr, kr = qs, ks
-    if rope is not None:
-        cos, sin, qpos, kpos = rope
-        qr = apply_rope(qs, cos, sin, qpos)
-        kr = apply_rope(ks, cos, sin, kpos)
     with torch.enable_grad():
+        qr, kr = qs, ks
+        if qk_norm is not None:
+            wq = qk_norm[0].to("cpu", dtype).detach().requires_grad_(True)
+            wk = qk_norm[1].to("cpu", dtype).detach().requires_grad_(True)
+            qr, kr = rms_norm(qr, wq, qk_norm[2]), rms_norm(kr, wk, qk_norm[2])
+        if rope is not None:
+            cos, sin, qpos, kpos = rope
+            qr = apply_rope(qr, cos, sin, qpos)
+            kr = apply_rope(kr, cos, sin, kpos)
         o = attention(qr, kr, vs, causal=causal, window_size=window_size, doc_ids=doc_ids,
                       alibi_slopes=alibi_slopes, base_attn_mask=base_attn_mask, scale=scale, dtype=dtype)
         o.backward(d_o.to("cpu", dtype))
+    if qk_norm is not None:
+        return qs.grad, ks.grad, vs.grad, wq.grad, wk.grad
     return qs.grad, ks.grad, vs.grad
 
 

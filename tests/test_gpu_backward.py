@@ -254,3 +254,123 @@ def test_gqa_layer_training_step_matches_cpu_reference():
         r = sd[n].grad
         e = ((g.cpu().float() - r).abs().max() / max(1.0, r.abs().max().item())).item()
         assert e <= 1e-4, f"{n}"
+
+
+def _xhat(x: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+
+
+def _check_norm_weight(dw, dw_ref, x, dn_ref, dtype, what):
+    """dw = sum over rows of x^ * dy: each term carries the error of dy (the
+    gradient of the normalized row, stored in the input dtype), so the bound
+    per head-dim element is sum_rows |x^| * (TOL + STORAGE * max|dy|)."""
+    xh = _xhat(x, 1e-6).reshape(-1, x.shape[-1]).abs().sum(0)
+    bound = xh * (TOL[dtype] + STORAGE[dtype] * dn_ref.abs().max().item())
+    err = (dw.cpu().float() - dw_ref.float()).abs()
+    worst = (err / bound).max().item()
+    print(f"{what}: max |d_w err| {err.max().item():.3e}, max |d_w| {dw_ref.abs().max().item():.3e}, "
+          f"err/bound {worst:.3f}", flush=True)
+    assert worst <= 1.0, f"{what}: weight gradient err {err.max().item()} over its bound"
+
+
+def _check_normed_rows(got, dx_ref, x, w, dn_ref, dtype, what, eps=1e-6):
+    """dx = r (g dy - x^ mean(x^ g dy)) (g = 1 + w) turns an error |d dy| <= e
+    of the normalized row's gradient (e = TOL + STORAGE max|dy|: dy is held in
+    the input dtype, as on the unfused path) into
+    |d dx_i| <= r (|g_i| + |x^_i| mean_j |x^_j g_j|) e, plus dx's own storage
+    rounding. A structural mistake (a wrong r, a dropped 1 +, a missing mean
+    term) errs by the size of dx itself."""
+    xf = x.float()
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    xh = xf * r
+    g = 1.0 + w.float()
+    e_dy = TOL[dtype] + STORAGE[dtype] * dn_ref.abs().max().item()
+    m = (xh * g).abs().mean(-1, keepdim=True)
+    bound = r * (g.abs() + xh.abs() * m) * e_dy + STORAGE[dtype] * dx_ref.abs().max().item()
+    err = (got.cpu().float() - dx_ref.float()).abs()
+    worst = (err / bound).max().item()
+    print(f"{what}: max err {err.max().item():.3e} (max |ref| {dx_ref.abs().max().item():.3e}), "
+          f"err/bound {worst:.3f}", flush=True)
+    assert worst <= 1.0, f"{what}: err {err.max().item()} over its propagated bound"
+
+
+def _norm_case(b, tq, tk, hq, hkv, d, dtype, *, rope, seed, varlen_lens=None):
+    eps = 1e-6
+    g = torch.Generator().manual_seed(seed + 100)
+    wq = torch.randn(d, generator=g) * 0.3
+    wk = torch.randn(d, generator=g) * 0.3
+    if varlen_lens is None:
+        q = _rand((b, tq, hq, d), dtype, seed)
+        k = _rand((b, tk, hkv, d), dtype, seed + 1)
+        v = _rand((b, tk, hkv, d), dtype, seed + 2)
+        d_o = _rand((b, tq, hq, d), dtype, seed + 3, std=1.0)
+        segs = [(None, None)]
+        kw = dict(causal=True)
+    else:
+        cu = torch.tensor([0] + list(np.cumsum(varlen_lens)), dtype=torch.int32)
+        tot = int(cu[-1])
+        q = _rand((tot, hq, d), dtype, seed)
+        k = _rand((tot, hkv, d), dtype, seed + 1)
+        v = _rand((tot, hkv, d), dtype, seed + 2)
+        d_o = _rand((tot, hq, d), dtype, seed + 3, std=1.0)
+        segs = list(zip(cu[:-1].tolist(), cu[1:].tolist()))
+        kw = dict(causal=True, cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(varlen_lens),
+                  max_seqlen_k=max(varlen_lens))
+        tq = tk = max(varlen_lens)
+    kw.update(q_norm_weight=wq.to(DEV), k_norm_weight=wk.to(DEV), norm_eps=eps)
+    if rope:
+        cos, sin = wl.rope_tables(tk + 8, d, 10000.0)
+        kw.update(rope_cos=cos.to(DEV), rope_sin=sin.to(DEV), rope_q=True, rope_k=True)
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = ops.attention_prefill(qg, kg, vg, return_lse=True, **kw)
+    dq, dk, dv, dwq, dwk = ops.attention_prefill_bwd(qg, kg, vg, o, lse, d_o.to(DEV), **kw)
+    torch.cuda.synchronize()
+    acc_wq, acc_wk = torch.zeros(d, dtype=torch.float64), torch.zeros(d, dtype=torch.float64)
+    dnq_max, dnk_max = 0.0, 0.0
+    for s, e in segs:
+        sl = slice(s, e)
+        qs, ks, vs, gs = ((x[sl][None] if s is not None else x) for x in (q, k, v, d_o))
+        okw = {}
+        if rope:
+            n_q, n_k = qs.shape[1], ks.shape[1]
+            okw["rope"] = (cos, sin, torch.arange(n_k - n_q, n_k), torch.arange(n_k))
+        rq, rk, rv, rwq, rwk = ref.attention_grads(qs.float(), ks.float(), vs.float(), gs.float(), causal=True,
+                                                   qk_norm=(wq, wk, eps), **okw)
+        got = [x[sl][None] if s is not None else x for x in (dq, dk, dv)]
+        what = f"norm d{d} {dtype} rope={rope} seg {s}:{e}"
+        _check(got[2:], (rv,), dtype, what)  # _check names its first tensor dq: here it is dv
+        acc_wq += rwq.double()
+        acc_wk += rwk.double()
+        # gradients of the normalized rows (dy of the bounds)
+        dn = ref.attention_grads(ref.rms_norm(qs.float(), wq, eps), ref.rms_norm(ks.float(), wk, eps), vs.float(),
+                                 gs.float(), causal=True, **okw)
+        _check_normed_rows(got[0], rq, qs, wq, dn[0], dtype, what + " dq")
+        _check_normed_rows(got[1], rk, ks, wk, dn[1], dtype, what + " dk")
+        dnq_max, dnk_max = max(dnq_max, dn[0].abs().max().item()), max(dnk_max, dn[1].abs().max().item())
+    _check_norm_weight(dwq, acc_wq, q, torch.tensor(dnq_max), dtype, f"norm d{d} {dtype} rope={rope} d_q_norm_weight")
+    _check_norm_weight(dwk, acc_wk, k, torch.tensor(dnk_max), dtype, f"norm d{d} {dtype} rope={rope} d_k_norm_weight")
+    return (dq, dk, dv, dwq, dwk), (qg, kg, vg, o, lse, d_o, kw)
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 64), (torch.bfloat16, 128), (torch.bfloat16, 256),
+                                     (torch.float16, 128), (torch.float32, 128), (torch.float32, 256)])
+@pytest.mark.parametrize("rope", [False, True])
+def test_backward_fused_qk_norm(dtype, d, rope):
+    """The fused QK-RMSNorm (goda's RMSNorm before RoPE, mint/nn/attn.py:57-60)
+    through the backward: dq / dk of the rows before the norm and both scales'
+    gradients against the oracle's autograd (fp32 at head_dim 256 runs the
+    generic kernels over materialized normalized rows)."""
+    _norm_case(2, 96, 96, 8, 2, d, dtype, rope=rope, seed=41)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_fused_qk_norm_varlen_mqa(dtype):
+    _norm_case(1, 0, 0, 6, 1, 128, dtype, rope=True, seed=43, varlen_lens=[40, 1, 75, 9])
+
+
+def test_backward_fused_qk_norm_weight_gradients_are_deterministic():
+    grads, (qg, kg, vg, o, lse, d_o, kw) = _norm_case(2, 300, 300, 8, 2, 128, torch.bfloat16, rope=True, seed=47)
+    again = ops.attention_prefill_bwd(qg, kg, vg, o, lse, d_o.to(DEV), **kw)
+    for a_, b_ in zip(grads[3:], again[3:]):
+        assert torch.equal(a_, b_)

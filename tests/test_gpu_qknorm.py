@@ -90,13 +90,30 @@ def test_kv_append_fused_k_norm(dtype, d):
         assert max_err(vc[i, p0 : p0 + tn], vn[i]) == 0.0
 
 
-def test_backward_rejects_fused_norm():
-    q = _rand((1, 16, 2, 64), torch.bfloat16, 1).to(DEV)
-    k = q[:, :, :1].contiguous()
-    w = torch.zeros(64, device=DEV)
-    o, lse = ops.attention_prefill(q, k, k, causal=True, q_norm_weight=w, return_lse=True)
-    with pytest.raises(Exception, match="forward only"):
-        ops.attention_prefill_bwd(q, k, k, o, lse, torch.ones_like(o), causal=True, q_norm_weight=w)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flashattention_trains_through_the_fused_norm(dtype):
+    """FlashAttention with qk_norm=(q_scale, k_scale, eps) and fused RoPE under
+    autograd: q, k, v and both scales get the oracle's gradients (the norm and
+    RoPE stay inside the kernels, forward and backward)."""
+    b, t, hq, hkv, d = 2, 70, 4, 2, 128
+    q, k, v = _rand((b, t, hq, d), dtype, 11, 2.0), _rand((b, t, hkv, d), dtype, 12, 2.0), _rand((b, t, hkv, d), dtype, 13)
+    d_o = _rand((b, t, hq, d), dtype, 14, std=1.0)
+    wq, wk = _rand((d,), torch.float32, 15, std=0.2), _rand((d,), torch.float32, 16, std=0.2)
+    cos, sin = wl.rope_tables(t, d, 10000.0)
+    qg, kg, vg = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    wqg, wkg = wq.to(DEV).requires_grad_(True), wk.to(DEV).requires_grad_(True)
+    o = FlashAttention()(qg, kg, vg, causal=True, rope=(cos.to(DEV), sin.to(DEV)), qk_norm=(wqg, wkg, EPS))
+    o.backward(d_o.to(DEV))
+    pos = torch.arange(t)
+    rq, rk, rv, rwq, rwk = ref.attention_grads(q.float(), k.float(), v.float(), d_o.float(), causal=True,
+                                               rope=(cos, sin, pos, pos), qk_norm=(wq, wk, EPS))
+    # relative to each gradient's size: the inputs' rms of 2 scales dq / dk by 1/2
+    # through the norm, and the scales' gradients sum every row
+    for name, got, want in (("dq", qg.grad, rq), ("dk", kg.grad, rk), ("dv", vg.grad, rv), ("dwq", wqg.grad, rwq),
+                            ("dwk", wkg.grad, rwk)):
+        e = max_err(got, want) / max(1.0, want.abs().max().item())
+        assert e <= (1e-5 if dtype == torch.float32 else 2e-2), f"{name}: {e}"
+    assert wqg.grad.dtype == torch.float32 and wqg.grad.shape == (d,)
 
 
 def test_generate_loop_with_fused_norm_matches_reference():

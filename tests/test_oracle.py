@@ -531,6 +531,43 @@ def test_planted_rms_norm_without_one_plus_is_caught():
     assert torch.allclose(ref.rms_norm(x, scale, 1e-6), lib, atol=1e-12)
 
 
+def test_autograd_oracle_through_qk_norm_matches_finite_differences():
+    """With the QK-RMSNorm before RoPE, dq / dk refer to the rows before the
+    norm and the scales get their own gradients: checked against finite
+    differences of brute-force attention over torch's library rms_norm and
+    brute-force RoPE."""
+    tq, tk, hq, hkv, d, base, eps = 3, 4, 2, 1, 4, 10000.0, 1e-6
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal((1, tq, hq, d))
+    k = rng.standard_normal((1, tk, hkv, d))
+    v = rng.standard_normal((1, tk, hkv, d))
+    wq = 0.3 * rng.standard_normal(d)
+    wk = 0.3 * rng.standard_normal(d)
+    d_o = rng.standard_normal((1, tq, hq, d))
+    qpos, kpos = np.arange(tk - tq, tk), np.arange(tk)
+    cos, sin = ref.rope_tables(8, d, base)
+    t = torch.from_numpy
+    dq, dk, dv, dwq, dwk = ref.attention_grads(
+        t(q), t(k), t(v), t(d_o), causal=True, rope=(cos.double(), sin.double(), t(qpos), t(kpos)),
+        qk_norm=(t(wq), t(wk), eps), dtype=F64,
+    )
+
+    def norm(x, w):
+        return torch.nn.functional.rms_norm(t(x), (d,), weight=1.0 + t(w), eps=eps).numpy()
+
+    def fwd(a, b_, c, wa, wb):
+        qa = brute.rope(norm(a, wa), qpos, base)
+        kb = brute.rope(norm(b_, wb), kpos, base)
+        return brute.attention(qa, kb, c, causal=True)[0]
+
+    fq, fk, fv, fwq, fwk = _loss_fd(fwd, [q, k, v, wq, wk], d_o)
+    # the fp32 cos/sin tables limit agreement to ~1e-7
+    for got, want in ((dq, fq), (dk, fk), (dv, fv), (dwq, fwq), (dwk, fwk)):
+        assert np.abs(got.numpy() - want).max() < 1e-5
+    # a dropped "1 +" in the norm's backward would scale dq by w / (1 + w)
+    assert np.abs(fq).max() > 1e-2
+
+
 @pytest.mark.parametrize("causal,alibi,tq,tk", [(True, False, 13, 13), (True, True, 9, 17), (False, False, 11, 7),
                                                 (False, True, 6, 6)])
 def test_chunked_grads_match_autograd_oracle(causal, alibi, tq, tk):
