@@ -591,7 +591,11 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], p1, dv[md]);
         dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
       }
-      lead_schedule<T, 4 * MD, 4>();
+      // All operand reads first: B's products share the matrix core with A's
+      // and wait on LDS latency if they read only a few products ahead
+      // (phase timestamps: B's 16 products spread over ~2100 clocks with
+      // reads 4 ahead, ~1400 with all 16 up front; dk/dv kernel -4%).
+      lead_schedule<T, 4 * MD, 4 * MD>();
     }
   });
 
