@@ -112,12 +112,16 @@ __device__ __forceinline__ const T* grow(const void* base, int64_t sb, int64_t s
 // Elements c..c+7 and c+D/2..c+D/2+7 of a q or k row, held by one of the
 // row's N consecutive lanes: goda's RMSNorm (weight w, or none) and then the
 // half-split rotation at `pos` (when `rot`), in fp32 and rounded once, as
-// the forward's pre-passes compute them. Every lane of the row's group must
-// call it (the norm's sum of squares is a group reduction).
+// the forward's pre-passes compute them. With `sc1`, `sc2` also the row times
+// `scale`, rounded once from the same fp32 values (the forward's q operand).
+// Every lane of the row's group must call it (the norm's sum of squares is a
+// group reduction).
 template <typename T, int D, int N>
 __device__ __forceinline__ void norm_rope_row(typename Vec<T>::v8& h1, typename Vec<T>::v8& h2, int c, const float* w,
-                                              float eps, bool rot, int pos, const goda_prefill_args& a) {
-  if (!w && !rot) return;
+                                              float eps, bool rot, int pos, const goda_prefill_args& a,
+                                              float scale = 0.f, typename Vec<T>::v8* sc1 = nullptr,
+                                              typename Vec<T>::v8* sc2 = nullptr) {
+  if (!w && !rot && !sc1) return;
   float x1[8], x2[8];
   float ss = 0.f;
 #pragma unroll
@@ -148,6 +152,10 @@ __device__ __forceinline__ void norm_rope_row(typename Vec<T>::v8& h1, typename 
   for (int e = 0; e < 8; ++e) {
     h1[e] = (T)x1[e];
     h2[e] = (T)x2[e];
+    if (sc1) {
+      (*sc1)[e] = (T)(x1[e] * scale);
+      (*sc2)[e] = (T)(x2[e] * scale);
+    }
   }
 }
 
@@ -165,7 +173,8 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
   if (i0 >= g.lq) return;
   const bool varlen = a.cu_seqlens_q != nullptr;
   const int diag = g.lk - g.lq;
-  __shared__ __align__(16) T qrows[kQRows][D + 8];
+  __shared__ __align__(16) T qrows[kQRows][D + 8];   // q for the transposed image (dK)
+  __shared__ __align__(16) T qsrows[kQRows][D + 8];  // q * scale * log2(e) for the row-major one (S)
   __shared__ __align__(16) T grows[kQRows][D + 8];
   const int tid = threadIdx.x;
   constexpr int HALF8 = D / 16;
@@ -185,20 +194,24 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
       g1 = ld_vec<v8>(gr + c);
       g2 = ld_vec<v8>(gr + c + D / 2);
     }
+    v8 qs1, qs2;
     norm_rope_row<T, D, HALF8>(q1, q2, c, a.q_norm_weight, a.norm_eps, i < g.lq && a.rope_q,
-                               i < g.lq ? rope_qpos(a, diag, i) : 0, a);
+                               i < g.lq ? rope_qpos(a, diag, i) : 0, a, p.scale_log2, &qs1, &qs2);
     st_vec<v8>(&qrows[r][c], q1);
     st_vec<v8>(&qrows[r][c + D / 2], q2);
+    st_vec<v8>(&qsrows[r][c], qs1);
+    st_vec<v8>(&qsrows[r][c + D / 2], qs2);
     st_vec<v8>(&grows[r][c], g1);
     st_vec<v8>(&grows[r][c + D / 2], g2);
   }
   __syncthreads();
 
   v8* img = reinterpret_cast<v8*>(p.qimg + q_tile_index(b, qt, hq, p.ntq, a.heads_q) * QI::BYTES);
-  // row-major images: chunk (c, r) at c*32 + r
+  // row-major images: chunk (c, r) at c*32 + r (q prescaled: the scores leave
+  // the matrix core in log2 units, as in the forward)
   for (int idx = tid; idx < QI::CH; idx += 256) {
     const int c = idx / kQRows, r = idx % kQRows;
-    img[QI::QA + idx] = ld_vec<v8>(&qrows[r][8 * c]);
+    img[QI::QA + idx] = ld_vec<v8>(&qsrows[r][8 * c]);
     img[QI::GA + idx] = ld_vec<v8>(&grows[r][8 * c]);
   }
   // transposed images: chunk (kc, d) at kc*D + d holds rows
@@ -502,7 +515,6 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       asm volatile("" : "+v"(kf[ks]));
       asm volatile("" : "+v"(vf[ks]));
     }
-    const float c = p.scale_log2;
     const bool key_ok = key < g.lk;
     QWalk cu(0, nq);
     uint32_t mword = 0;
@@ -519,7 +531,9 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         cu.next();
         const v8* st = stage(it);
         const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
-        // S [rows][keys] and dP: two interleaved accumulation chains.
+        // S [rows][keys] and dP: two interleaved accumulation chains (the q
+        // image holds q * scale * log2(e): S leaves the matrix core in log2
+        // units).
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -528,7 +542,10 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         }
         lead_schedule<T, 2 * KS, 4>();
         // P and dS; visibility as a range of the register's row offset
-        // off = row - (q0 + 4 hi).
+        // off = row - (q0 + 4 hi). (Starting the accumulators at -lse2 and
+        // -delta, as the head_dim-256 and dq kernels do, saves two VALU
+        // instructions per entry but makes the products wait for the row
+        // statistics' LDS reads: 2% slower here.)
         const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
         const int rel = q0 + 4 * hi;
         int lo_lim = -1, hi_lim = g.lq - 1 - rel;
@@ -546,7 +563,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * gq + e;
-            float t = s[r] * c;
+            float t = s[r];
             if (ALIBI) t += base - slope2 * (float)(8 * gq + e);
             pr[r] = fast_exp2(t - l2[e]);
             ds[r] = pr[r] * (dp[r] - dl[e]);
@@ -732,7 +749,6 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
   };
 
-  const float c = p.scale_log2;
   QWalk cu(it0, nq), nw(it0, nq);
   if (it0 < it1) {
     const v8* src = src_of(cu);
@@ -767,8 +783,22 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     uint32_t mword = 0;
     if (MASK && key < g.lk)
       mword = p.mask_t[b * p.mt_stride_b + hq * p.mt_stride_h + (int64_t)key * p.ntq + qt] >> (4 * hi);
-    // S and dP: two independent accumulation chains, interleaved.
-    f32x16 s = f32x16{}, dp = f32x16{};
+    // S and dP: two independent accumulation chains, interleaved, starting
+    // at -lse2 (+ the ALiBi bias) and -delta (the q image is prescaled, as in
+    // the 8-wave kernel). Register r is row off = 8 (r/4) + r%4 past q0 + 4 hi.
+    const int rel = q0 + 4 * hi;
+    const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
+    f32x16 s, dp;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
+      const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[4 * gq + e] = (ALIBI ? base - slope2 * (float)(8 * gq + e) : 0.f) - l2[e];
+        dp[4 * gq + e] = -dl[e];
+      }
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
@@ -778,9 +808,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     store_next(0);
     load_part(nsrc, 1);
 
-    // P and dS; visibility as a range of the register's row offset
-    // off = row - (q0 + 4 hi).
-    const int rel = q0 + 4 * hi;
+    // P and dS; visibility as a range of the register's row offset.
     int lo_lim = -1, hi_lim = g.lq - 1 - rel;
     if (a.causal) lo_lim = key - diag - rel;
     if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
@@ -789,20 +817,11 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     // some (as in the 8-wave kernel)
     uint32_t vis = key_ok ? range_bits(lo_lim, hi_lim) : 0u;
     if (MASK) vis &= mword;
-    const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
     float pr[16], ds[16];
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
-      const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * gq + e;
-        float t = s[r] * c;
-        if (ALIBI) t += base - slope2 * (float)(8 * gq + e);
-        pr[r] = fast_exp2(t - l2[e]);
-        ds[r] = pr[r] * (dp[r] - dl[e]);
-      }
+    for (int r = 0; r < 16; ++r) {
+      pr[r] = fast_exp2(s[r]);
+      ds[r] = pr[r] * dp[r];
     }
     if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
 #pragma unroll
@@ -998,7 +1017,6 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     asm volatile("" : "+v"(gf[ks]));
   }
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
-  const float c = p.scale_log2;
   // The caller's mask row of this lane's query row (rows past the sequence
   // read the last row's bits and are masked anyway): one word per key tile.
   const uint32_t* mrow = MASK ? mask_row(a, b, hq, min(i, g.lq - 1)) : nullptr;
@@ -1036,10 +1054,20 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     const int kvb = (j_lo + it) * kBKV;
     const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * KI::BYTES);
     const uint32_t mword = MASK ? mrow[j_lo + it] >> (4 * hi) : 0u;
-    // S^T[keys][rows] and dP^T
+    // S^T[keys][rows] and dP^T, starting at -lse2 (+ the ALiBi bias of
+    // register r's key offset off = 8 (r/4) + r%4 past kvb + 4 hi) and at
+    // -delta: the q operand is prescaled (scale * log2(e)), so they leave the
+    // matrix core as the exponents of P and as dP - delta.
+    const int rel = kvb + 4 * hi;
+    const float base = ALIBI ? slope2 * (float)(rel - iabs) : 0.f;
     f32x16 s[MT], dp[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) s[mt] = dp[mt] = f32x16{};
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[mt][r] = (ALIBI ? base + slope2 * (float)(32 * mt + 8 * (r >> 2) + (r & 3)) : 0.f) - l2;
+        dp[mt][r] = -dl;
+      }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -1049,7 +1077,6 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
       }
     lead_schedule<T, 2 * KS * MT, 4>();
     // masks as ranges of the register's key offset off = key - (kvb + 4 hi)
-    const int rel = kvb + 4 * hi;
     int hi_lim = g.lk - 1 - rel;
     if (a.causal) hi_lim = min(hi_lim, iabs - rel);
     const int lo_lim = use_window ? iabs - a.window_left - rel : 0;
@@ -1060,14 +1087,9 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     static_assert(MT == 1, "one 32-bit visibility word per key tile");
     uint32_t vis = row_ok ? range_bits(lo_lim, hi_lim) : 0u;
     if (MASK) vis &= mword;
-    const float base = ALIBI ? slope2 * (float)(rel - iabs) : 0.f;
     float ds[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float t = s[0][r] * c;
-      if (ALIBI) t += base + slope2 * (float)(8 * (r >> 2) + (r & 3));
-      ds[r] = fast_exp2(t - l2) * (dp[0][r] - dl);
-    }
+    for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[0][r]) * dp[0][r];
     if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) ds[r] = keep_if_bit(ds[r], vis, 8 * (r >> 2) + (r & 3), 0.f);
