@@ -804,7 +804,10 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
       dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
     }
-    lead_schedule<T, 2 * KS, 4>();
+    // One wave per SIMD: nothing else hides a product's LDS operand latency,
+    // so the reads run 12 products ahead here (4 ahead: 4.54 ms for the
+    // cfg3-shape dk/dv, 8: 3.64, 10-16: 3.33-3.36).
+    lead_schedule<T, 2 * KS, 12>();
     store_next(0);
     load_part(nsrc, 1);
 
@@ -839,7 +842,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
       dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
     }
-    lead_schedule<T, 2 * MD, 4>();
+    lead_schedule<T, 2 * MD, 12>();
     store_next(2);
     load_part(nsrc, 3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
@@ -848,7 +851,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
       dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
     }
-    lead_schedule<T, 2 * MD, 4>();
+    lead_schedule<T, 2 * MD, 12>();
     store_next(3);
     ring_barrier();
   }
