@@ -345,6 +345,26 @@ __global__ void __launch_bounds__(256) bwd_mask_t_kernel(const BwdParams p) {
   }
 }
 
+// A phase of NJ products, each with one LDS operand: the operands of the
+// first L products are read first, each product's register is refilled with
+// the operand L products later, and scheduling fences keep that order (left
+// alone, the compiler moves every read next to its product, leaving about one
+// in flight; `lead_schedule` asks for the order but is not always honoured).
+template <int NJ, int L, typename V, typename Src, typename Prod>
+__device__ __forceinline__ void prefetched_products(Src src, Prod prod) {
+  constexpr int P = L < NJ ? L : NJ;
+  V op[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) op[j] = src(j);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    prod(j, op[j % P]);
+    if (j + P < NJ) op[j % P] = src(j + P);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
 // run LEAD MFMAs ahead (not all hoisted, which would hold 4 registers each).
 template <typename T, int NM, int LEAD>
@@ -535,12 +555,14 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         // image holds q * scale * log2(e): S leaves the matrix core in log2
         // units).
         f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
-          dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
-        }
-        lead_schedule<T, 2 * KS, 4>();
+        prefetched_products<2 * KS, 4, v8>(
+            [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + l32]; },
+            [&](int j, const v8& o) {
+              if (j & 1)
+                dp = mfma32(o, vf[j >> 1], dp);
+              else
+                s = mfma32(o, kf[j >> 1], s);
+            });
         // P and dS; visibility as a range of the register's row offset
         // off = row - (q0 + 4 hi). (Starting the accumulators at -lse2 and
         // -delta, as the head_dim-256 and dq kernels do, saves two VALU
@@ -598,21 +620,22 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       const v8* st = stage(it - 1);
       const v8 p0 = xchg(it - 1, 0), p1 = xchg(it - 1, 1);
       const v8 d0 = xchg(it - 1, 2), d1 = xchg(it - 1, 3);
-#pragma unroll
-      for (int md = 0; md < MD; ++md) {
-        dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], p0, dv[md]);
-        dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
-      }
-#pragma unroll
-      for (int md = 0; md < MD; ++md) {
-        dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], p1, dv[md]);
-        dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
-      }
-      // All operand reads first: B's products share the matrix core with A's
-      // and wait on LDS latency if they read only a few products ahead
-      // (phase timestamps: B's 16 products spread over ~2100 clocks with
-      // reads 4 ahead, ~1400 with all 16 up front; dk/dv kernel -4%).
-      lead_schedule<T, 4 * MD, 4 * MD>();
+      // Operand reads 8 products ahead (A's 4): with the matrix core shared
+      // with A, B's products otherwise wait on LDS latency (phase
+      // timestamps: B's 16 products spread over ~2100 clocks with about one
+      // read in flight). j: half = j / (2 MD), md = (j / 2) % MD, odd: dK.
+      prefetched_products<4 * MD, 8, v8>(
+          [&](int j) {
+            const int half = j / (2 * MD), md = (j >> 1) % MD;
+            return st[((j & 1) ? QI::QT : QI::GT) + (2 * half + hi) * D + 32 * md + l32];
+          },
+          [&](int j, const v8& o) {
+            const int half = j / (2 * MD), md = (j >> 1) % MD;
+            if (j & 1)
+              dk[md] = mfma32(o, half ? d1 : d0, dk[md]);
+            else
+              dv[md] = mfma32(o, half ? p1 : p0, dv[md]);
+          });
     }
   });
 
@@ -668,6 +691,10 @@ constexpr int kWideParts = 4;
 
 template <typename T, int D, bool ALIBI, bool MASK>
 __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const BwdParams p) {
+  // Operand reads in flight per product phase: one wave per SIMD, nothing
+  // else hides their LDS latency (cfg3-shape dk/dv: 4.54 ms with about one in
+  // flight, 3.04 with 4; 8 or more spill).
+  constexpr int WL = 4;
   typedef typename Vec<T>::v8 v8;
   typedef typename Vec<T>::v4 v4;
   typedef QImg<T, D> QI;
@@ -799,15 +826,16 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
         dp[4 * gq + e] = -dl[e];
       }
     }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s = mfma32(st[QI::QA + (2 * ks + hi) * kQRows + l32], kf[ks], s);
-      dp = mfma32(st[QI::GA + (2 * ks + hi) * kQRows + l32], vf[ks], dp);
-    }
     // One wave per SIMD: nothing else hides a product's LDS operand latency,
-    // so the reads run 12 products ahead here (4 ahead: 4.54 ms for the
-    // cfg3-shape dk/dv, 8: 3.64, 10-16: 3.33-3.36).
-    lead_schedule<T, 2 * KS, 12>();
+    // so the reads run WL products ahead.
+    prefetched_products<2 * KS, WL, v8>(
+        [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + l32]; },
+        [&](int j, const v8& o) {
+          if (j & 1)
+            dp = mfma32(o, vf[j >> 1], dp);
+          else
+            s = mfma32(o, kf[j >> 1], s);
+        });
     store_next(0);
     load_part(nsrc, 1);
 
@@ -837,21 +865,15 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     store_next(1);
     load_part(nsrc, 2);
     const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
-#pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      dv[md] = mfma32(st[QI::GT + hi * D + 32 * md + l32], pp0, dv[md]);
-      dv[md] = mfma32(st[QI::GT + (2 + hi) * D + 32 * md + l32], pp1, dv[md]);
-    }
-    lead_schedule<T, 2 * MD, 12>();
+    prefetched_products<2 * MD, WL, v8>(
+        [&](int j) { return st[QI::GT + (2 * (j & 1) + hi) * D + 32 * (j >> 1) + l32]; },
+        [&](int j, const v8& o) { dv[j >> 1] = mfma32(o, (j & 1) ? pp1 : pp0, dv[j >> 1]); });
     store_next(2);
     load_part(nsrc, 3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
-#pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      dk[md] = mfma32(st[QI::QT + hi * D + 32 * md + l32], d0, dk[md]);
-      dk[md] = mfma32(st[QI::QT + (2 + hi) * D + 32 * md + l32], d1, dk[md]);
-    }
-    lead_schedule<T, 2 * MD, 12>();
+    prefetched_products<2 * MD, WL, v8>(
+        [&](int j) { return st[QI::QT + (2 * (j & 1) + hi) * D + 32 * (j >> 1) + l32]; },
+        [&](int j, const v8& o) { dk[j >> 1] = mfma32(o, (j & 1) ? d1 : d0, dk[j >> 1]); });
     store_next(3);
     ring_barrier();
   }
@@ -968,6 +990,10 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
   constexpr int MD = D / 32;
   constexpr int MT = kBKV / 32;   // 32-key blocks of S^T
   constexpr int KS2 = kBKV / 16;  // k-steps of dQ^T over keys
+  // Operand reads in flight per product phase with one wave per SIMD (cfg3
+  // shape: 2.51 -> 1.99 ms); two waves per SIMD hide each other's latency and
+  // keep the scheduler's order (fenced prefetch there: +1-2%).
+  constexpr int QL = DqShape<T, D>::WIDE ? 4 : 0;
   constexpr int LOADS = (KI::CHUNKS + kWavesDq * 64 - 1) / (kWavesDq * 64);
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -1071,14 +1097,25 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
         s[mt][r] = (ALIBI ? base + slope2 * (float)(32 * mt + 8 * (r >> 2) + (r & 3)) : 0.f) - l2;
         dp[mt][r] = -dl;
       }
+    if constexpr (QL > 0) {
+      prefetched_products<2 * KS, QL, v8>(
+          [&](int j) { return st[((j & 1) ? KI::VA : KI::KA) + (2 * (j >> 1) + hi) * kBKV + l32]; },
+          [&](int j, const v8& o) {
+            if (j & 1)
+              dp[0] = mfma32(o, gf[j >> 1], dp[0]);
+            else
+              s[0] = mfma32(o, qf[j >> 1], s[0]);
+          });
+    } else {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + l32], qf[ks], s[mt]);
-        dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + l32], gf[ks], dp[mt]);
-      }
-    lead_schedule<T, 2 * KS * MT, 4>();
+        for (int mt = 0; mt < MT; ++mt) {
+          s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + l32], qf[ks], s[mt]);
+          dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + l32], gf[ks], dp[mt]);
+        }
+      lead_schedule<T, 2 * KS * MT, 4>();
+    }
     // masks as ranges of the register's key offset off = key - (kvb + 4 hi)
     int hi_lim = g.lk - 1 - rel;
     if (a.causal) hi_lim = min(hi_lim, iabs - rel);
@@ -1101,12 +1138,18 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     dsf[0] = pack8<v8, T>(ds);
     dsf[1] = pack8<v8, T>(ds + 8);
     // dQ^T += K^T dS^T
+    if constexpr (QL > 0) {
+      prefetched_products<KS2 * MD, QL, v8>(
+          [&](int j) { return st[KI::KT + (2 * (j / MD) + hi) * D + 32 * (j % MD) + l32]; },
+          [&](int j, const v8& o) { dq[j % MD] = mfma32(o, dsf[j / MD], dq[j % MD]); });
+    } else {
 #pragma unroll
-    for (int ks2 = 0; ks2 < KS2; ++ks2)
+      for (int ks2 = 0; ks2 < KS2; ++ks2)
 #pragma unroll
-      for (int md = 0; md < MD; ++md)
-        dq[md] = mfma32(st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32], dsf[ks2], dq[md]);
-    lead_schedule<T, KS2 * MD, 4>();
+        for (int md = 0; md < MD; ++md)
+          dq[md] = mfma32(st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32], dsf[ks2], dq[md]);
+      lead_schedule<T, KS2 * MD, 4>();
+    }
   };
 
   if (n > 0) {
