@@ -103,6 +103,23 @@ struct QWalk {
   }
 };
 
+// The same steps in the order the dk/dv kernels walk them: query tile
+// outermost, from the last tile down, the group's heads innermost (step it is
+// head it % g of tile nq - 1 - it / g). Every key block of a KV head then
+// reads the same tile images in the same order from the same starting tile,
+// whatever its causal first tile, so the blocks running at once share them
+// in L2.
+struct QWalkDown {
+  int h, q, g;
+  __device__ __forceinline__ QWalkDown(int it, int nq, int g_) : h(it % g_), q(nq - 1 - it / g_), g(g_) {}
+  __device__ __forceinline__ void next() {
+    if (++h == g) {
+      h = 0;
+      --q;
+    }
+  }
+};
+
 template <typename T>
 __device__ __forceinline__ const T* grow(const void* base, int64_t sb, int64_t st, int64_t sh, bool varlen, int b,
                                          int64_t row, int h) {
@@ -482,7 +499,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
 
   v8 stg[LOADS];
   v8 stg_stat;
-  QWalk ld(0, nq);  // the next tile to load; loads come in walk order
+  QWalkDown ld(0, nq, p.group);  // the next tile to load; loads come in walk order
   auto tile_load = [&]() {
     const int64_t t = q_tile_index(b, qt_lo + ld.q, hk * p.group + ld.h, p.ntq, a.heads_q);
     const v8* src = reinterpret_cast<const v8*>(p.qimg + t * QI::BYTES);
@@ -536,7 +553,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       asm volatile("" : "+v"(vf[ks]));
     }
     const bool key_ok = key < g.lk;
-    QWalk cu(0, nq);
+    QWalkDown cu(0, nq, p.group);
     uint32_t mword = 0;
     auto pre = [&](int it) {
       // the caller's mask bits of this key for the tile's 32 rows
