@@ -438,8 +438,14 @@ struct DkvSmem {
 // 1.19-1.23x the ideal at the cfg2 shape); here units go in chunks of
 // kOrderChunk, heaviest block of every unit of the chunk first (1.0x).
 // Measured: cfg2-shape backward 13.5 -> 10.7 ms, cfg3 shape 9.2 -> 6.4 ms
-// (chunks of 8, 16 and 32 alike; 4: 10.7 and 7.3 ms).
-constexpr int kOrderChunk = 16;
+// (chunks of 8, 16 and 32 alike then; 4: 10.7 and 7.3 ms).
+// Chunks of 8: consecutive workgroups go round-robin to the 8 XCDs, so every
+// block of one unit runs on the same XCD and each XCD runs one unit at a
+// time. With the dk/dv walk that reads the same query tiles in every key
+// block of a unit, one unit per XCD halves the distinct tiles streaming
+// through each L2 (16: two units per XCD): cfg2-shape dk/dv 5.10 -> 4.89 ms,
+// dq 2.99 -> 2.89 ms.
+constexpr int kOrderChunk = 8;
 __device__ __forceinline__ void chunked_order(int lin, int nblk, int units, int& unit, int& blk) {
   const int base = lin / (kOrderChunk * nblk) * kOrderChunk;
   const int cc = min(kOrderChunk, units - base);

@@ -118,7 +118,7 @@ def test_backward_d256_paths(dtype):
 
 
 def test_backward_workgroup_order_partial_chunks():
-    """The dk/dv and dq grids are walked in chunks of 16 (head group or pair)
+    """The dk/dv and dq grids are walked in chunks of 8 (head group or pair)
     units, heaviest block of each unit first; unit counts that leave a partial
     last chunk (3 x 6 = 18 units at head_dim 128; 5 x 2 x splits at 256 with
     the split dk/dv walk) must still visit every block exactly once."""
