@@ -8,11 +8,14 @@
 //
 // Four launches:
 //   1. pack_q_bwd_kernel: per (32-row query tile, query head, sequence),
-//      the operand images of rotated q and of dO, both row-major
+//      the row-major operand images of rotated q (prescaled) and of dO
 //      ("chunk-column-major" [D/8][32] 16-byte chunks, the A operand of a
-//      product over head_dim) and transposed ([32/8][D] chunks with the rows
-//      of each 16-row group in kPermKey order, the A operand of a product
-//      over rows), plus the row statistics lse*log2(e) and delta.
+//      product over head_dim), plus the row statistics lse*log2(e) and
+//      delta; for the one-wave dk/dv kernel (head_dim 256, fp32) also the
+//      transposed images ([32/8][D] chunks with the rows of each 16-row
+//      group in kPermKey order, the A operand of a product over rows). The
+//      split dk/dv kernel reads those operands out of the row-major images
+//      with transposing LDS reads (ds_read_b64_tr_b16).
 //   2. pack_kv_bwd_kernel: per (32-key tile, KV head, sequence), the
 //      row-major images of rotated k and of v and the transposed image of k.
 //   3. bwd_dkv_mfma_kernel: one workgroup of 8 waves per 128 keys of a KV
@@ -23,9 +26,9 @@
 //      of a pair computes S, dP, P and dS and hands P and dS to the other
 //      through LDS, which accumulates dV and dK one tile behind:
 //        S    [rows][keys] = Q K^T        A = Q image,   B = k (registers)
-//        dV^T [d][keys]   += dO^T P        A = dO^T image, B = P (packed S)
+//        dV^T [d][keys]   += dO^T P        A = dO^T (transposing reads), B = P (packed S)
 //        dP   [rows][keys] = dO V^T        A = dO image,  B = v (registers)
-//        dK^T [d][keys]   += Q^T dS        A = Q^T image, B = dS (packed)
+//        dK^T [d][keys]   += Q^T dS        A = Q^T (transposing reads), B = dS (packed)
 //      head_dim 256 (bwd_dkv_wide_kernel): a wave needs both operand sets and
 //      both accumulators (~450 registers), so four waves, one per SIMD, each
 //      owning 32 keys and doing all four products; with few key blocks the
@@ -63,14 +66,26 @@ struct DqShape {
 };
 
 // Images are counted in 8-element chunks (16 bytes, or 32 for fp32).
+// The transposed q and dO images (QT, GT) exist only where the one-wave dk/dv
+// kernel reads them (head_dim 256, fp32); the split dk/dv kernel reads its
+// transposed operands out of the row-major images with transposing LDS reads.
 template <typename T, int D>
 struct QImg {
   static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);
   static constexpr int CH = D / 8 * kQRows;  // chunks of one image
+  static constexpr bool HAS_T = DqShape<T, D>::WIDE;
+  static constexpr int NIMG = HAS_T ? 4 : 2;
   static constexpr int QA = 0, GA = CH, QT = 2 * CH, GT = 3 * CH;
-  static constexpr int STAT = 4 * CH;        // lse2[32] then delta[32]: 256 bytes
+  // Row-major images: chunk (c, r) (head-dim 8c..8c+7 of row r) at
+  // c*32 + (r ^ SWZ*(c%2)). Without the transposed images, a transposing read
+  // of 16 lanes covers rows r..r+3 of two adjacent chunk columns, 512 bytes
+  // apart (the same LDS banks); swapping the 4-row halves of every odd column
+  // puts them on disjoint banks. A 32-row column read stays one contiguous
+  // 512-byte block.
+  static constexpr int SWZ = HAS_T ? 0 : 4;
+  static constexpr int STAT = NIMG * CH;     // lse2[32] then delta[32]: 256 bytes
   static constexpr int STAT_CH = 256 / CHB;
-  static constexpr int CHUNKS = 4 * CH + STAT_CH;
+  static constexpr int CHUNKS = NIMG * CH + STAT_CH;
   static constexpr int64_t BYTES = (int64_t)CHUNKS * CHB;
 };
 
@@ -228,11 +243,13 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
   // the matrix core in log2 units, as in the forward)
   for (int idx = tid; idx < QI::CH; idx += 256) {
     const int c = idx / kQRows, r = idx % kQRows;
-    img[QI::QA + idx] = ld_vec<v8>(&qsrows[r][8 * c]);
-    img[QI::GA + idx] = ld_vec<v8>(&grows[r][8 * c]);
+    const int at = c * kQRows + (r ^ (QI::SWZ * (c & 1)));
+    img[QI::QA + at] = ld_vec<v8>(&qsrows[r][8 * c]);
+    img[QI::GA + at] = ld_vec<v8>(&grows[r][8 * c]);
   }
   // transposed images: chunk (kc, d) at kc*D + d holds rows
   // 16*(kc/2) + kPermKey(8*(kc%2) + e)
+  if constexpr (QI::HAS_T)
   for (int idx = tid; idx < QI::CH; idx += 256) {
     const int kc = idx / D, d = idx % D;
     const int r0 = 16 * (kc / 2);
@@ -469,8 +486,9 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   typedef KVImg<T, D> KI;
   constexpr int KS = D / 16;  // k-steps over head_dim
   constexpr int MD = D / 32;  // 32-wide head_dim tiles of dK^T / dV^T
-  constexpr int LOADS = 4 * QI::CH / (kWavesKv * 64);
-  static_assert(4 * QI::CH % (kWavesKv * 64) == 0, "tile must split over the waves");
+  static_assert(!QI::HAS_T && sizeof(T) == 2, "B's operands come from transposing reads of 16-bit images");
+  constexpr int LOADS = QI::NIMG * QI::CH / (kWavesKv * 64);
+  static_assert(QI::NIMG * QI::CH % (kWavesKv * 64) == 0, "tile must split over the waves");
   extern __shared__ __align__(16) unsigned char smem[];
   v8* xbuf = reinterpret_cast<v8*>(smem + DkvSmem<T, D>::RING);
 
@@ -579,7 +597,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         // units).
         f32x16 s = f32x16{}, dp = f32x16{};
         prefetched_products<2 * KS, 4, v8>(
-            [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + l32]; },
+            [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + (l32 ^ (QI::SWZ * hi))]; },
             [&](int j, const v8& o) {
               if (j & 1)
                 dp = mfma32(o, vf[j >> 1], dp);
@@ -638,9 +656,30 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   f32x16 dv[MD], dk[MD];
 #pragma unroll
   for (int md = 0; md < MD; ++md) dv[md] = dk[md] = f32x16{};
+  // B's A operands (dO^T, q^T: lane l holds head-dim 32 md + l%32 over the 8
+  // rows that P's and dS's packed registers of its lane half give, kPermKey
+  // order: 16 half + 4 hi + {0..3, 8..11}) come from the row-major images by
+  // two ds_read_b64_tr_b16 each. That instruction hands lane j of a 16-lane
+  // group element j%4 of the 8-byte segments read by lanes j/4 + 4e, e = 0..3:
+  // lane s reads row 16 half + 8 k + 4 hi + s/4 at head-dim
+  // 32 md + 16 ((l/16)%2) + 4 (s%4), so lane j receives rows
+  // 16 half + 8 k + 4 hi + e at head-dim 32 md + l%32. Row r, head-dim d of
+  // an image sits at byte ((d/8)*32 + (r ^ 4*((d/8)%2)))*16 + (d%8)*2.
+  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int tr_row = 4 * (hi ^ (QI::SWZ ? (tr_d >> 3) & 1 : 0)) + ((lane & 15) >> 2);  // column parity swizzle
+  const int tr_lane = ((tr_d >> 3) * kQRows + tr_row) * 16 + (tr_d & 7) * 2;
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  auto tr_operand = [&](const unsigned char* img, int half, int md) {
+    const unsigned char* base = img + tr_lane + md * (4 * kQRows * 16) + half * 256;
+    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(base));
+    const s4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(base + 128));
+    typedef short s8 __attribute__((ext_vector_type(8)));
+    const s8 v = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(v8, v);
+  };
   walk([](int) {}, [&](int it) {
     if (it > 0) {
-      const v8* st = stage(it - 1);
+      const unsigned char* st = reinterpret_cast<const unsigned char*>(stage(it - 1));
       const v8 p0 = xchg(it - 1, 0), p1 = xchg(it - 1, 1);
       const v8 d0 = xchg(it - 1, 2), d1 = xchg(it - 1, 3);
       // Operand reads 8 products ahead (A's 4): with the matrix core shared
@@ -650,7 +689,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       prefetched_products<4 * MD, 8, v8>(
           [&](int j) {
             const int half = j / (2 * MD), md = (j >> 1) % MD;
-            return st[((j & 1) ? QI::QT : QI::GT) + (2 * half + hi) * D + 32 * md + l32];
+            return tr_operand(st + ((j & 1) ? QI::QA : QI::GA) * QI::CHB, half, md);
           },
           [&](int j, const v8& o) {
             const int half = j / (2 * MD), md = (j >> 1) % MD;
@@ -677,10 +716,11 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   const bool rot = a.rope_k && key < g.lk;
   const int pos = a.rope_k_offset + key;
   // dk: pairs of head-dim blocks (md, md + MD/2: the rotation's partners),
-  // scaled and rotated back.
+  // scaled and rotated back. dK^T accumulated against the row-major q image,
+  // which holds q * scale * log2(e): dk = scale * (dS^T q) = ln(2) * dK^T.
 #pragma unroll
   for (int md = 0; md < MD / 2; ++md) {
-    f32x16 x1 = dk[md] * a.softmax_scale, x2 = dk[md + MD / 2] * a.softmax_scale;
+    f32x16 x1 = dk[md] * kLn2, x2 = dk[md + MD / 2] * kLn2;
     if (rot) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -1053,8 +1093,8 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     const v8* img = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, wrow0 / kQRows, hq, p.ntq, a.heads_q) * QI::BYTES);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = img[QI::QA + (2 * ks + hi) * kQRows + l32];
-      gf[ks] = img[QI::GA + (2 * ks + hi) * kQRows + l32];
+      qf[ks] = img[QI::QA + (2 * ks + hi) * kQRows + (l32 ^ (QI::SWZ * hi))];
+      gf[ks] = img[QI::GA + (2 * ks + hi) * kQRows + (l32 ^ (QI::SWZ * hi))];
     }
     const float* stat = reinterpret_cast<const float*>(img + QI::STAT);
     l2 = stat[l32];
