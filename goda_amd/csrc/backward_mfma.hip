@@ -17,7 +17,9 @@
 //      split dk/dv kernel reads those operands out of the row-major images
 //      with transposing LDS reads (ds_read_b64_tr_b16).
 //   2. pack_kv_bwd_kernel: per (32-key tile, KV head, sequence), the
-//      row-major images of rotated k and of v and the transposed image of k.
+//      row-major images of rotated k and of v and, for the one-wave kernels,
+//      the transposed image of k (the split path's dq reads k^T out of the
+//      row-major image with transposing LDS reads).
 //   3. bwd_dkv_mfma_kernel: one workgroup of 8 waves per 128 keys of a KV
 //      head, in pairs (two waves of one SIMD) that share 32 keys; the pair
 //      pins the k and v operands of its keys and walks the query tiles of
@@ -40,7 +42,7 @@
 //      dO operands of its 32 rows and walks the key tiles:
 //        S^T  [keys][rows] = K Q^T         A = k image,   B = q (registers)
 //        dP^T [keys][rows] = V dO^T        A = v image,   B = dO (registers)
-//        dQ^T [d][rows]   += K^T dS^T      A = K^T image, B = dS^T (packed)
+//        dQ^T [d][rows]   += K^T dS^T      A = K^T (image or transposing reads), B = dS^T (packed)
 // A packed accumulator becomes a B operand directly because the transposed
 // images hold their rows / keys in the accumulator's register order
 // (kPermKey). With the log-sum-exp known there is no online softmax.
@@ -89,14 +91,44 @@ struct QImg {
   static constexpr int64_t BYTES = (int64_t)CHUNKS * CHB;
 };
 
+// Key-side images: row-major k and v (with the query images' odd-column
+// swizzle) and, for the one-wave kernels only, the transposed k; the dq
+// kernel of the split path reads k^T out of the row-major image.
 template <typename T, int D>
 struct KVImg {
   static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);
   static constexpr int CH = D / 8 * kBKV;
+  static constexpr bool HAS_T = DqShape<T, D>::WIDE;
+  static constexpr int NIMG = HAS_T ? 3 : 2;
+  static constexpr int SWZ = HAS_T ? 0 : 4;
   static constexpr int KA = 0, VA = CH, KT = 2 * CH;
-  static constexpr int CHUNKS = 3 * CH;
+  static constexpr int CHUNKS = NIMG * CH;
   static constexpr int64_t BYTES = (int64_t)CHUNKS * CHB;
 };
+
+// A operand of a product over the 32 rows (or keys) of a row-major image
+// tile, i.e. the transposed tile, for 16-bit images with the odd-column
+// swizzle: lane l gets head-dim 32 md + l%32 over rows 16 half + 4 (l/32) +
+// {0..3, 8..11}, the order of the packed accumulator registers of its lane
+// half (kPermKey). Two ds_read_b64_tr_b16: that instruction hands lane j of a
+// 16-lane group element j%4 of the 8-byte segments read by lanes j/4 + 4e,
+// e = 0..3; lane s reads row 16 half + 8 k + 4 (l/32) + s/4 at head-dim
+// 32 md + 16 ((l/16)%2) + 4 (s%4), so lane j receives rows
+// 16 half + 8 k + 4 (l/32) + e at head-dim 32 md + l%32. Row r, head-dim d
+// sits at byte ((d/8)*32 + (r ^ 4*((d/8)%2)))*16 + (d%8)*2 of the image.
+template <typename V>
+__device__ __forceinline__ V tr_operand(const unsigned char* img, int lane, int half, int md) {
+  static_assert(sizeof(V) == 16, "16-bit operands");
+  const int hi = lane >> 5;
+  const int d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int row = 4 * (hi ^ ((d >> 3) & 1)) + ((lane & 15) >> 2);  // odd-column swizzle
+  const unsigned char* base = img + ((d >> 3) * 32 + row) * 16 + (d & 7) * 2 + md * (4 * 32 * 16) + half * 256;
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef short s8 __attribute__((ext_vector_type(8)));
+  const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(base));
+  const s4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(base + 128));
+  return __builtin_bit_cast(V, (s8)__builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 __device__ __forceinline__ int64_t q_tile_index(int b, int qt, int hq, int ntq, int heads_q) {
   return ((int64_t)b * ntq + qt) * heads_q + hq;
@@ -337,9 +369,11 @@ __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
   v8* img = reinterpret_cast<v8*>(p.kvimg + kv_tile_index(b, j, hk, p.ntk, a.heads_kv) * KI::BYTES);
   for (int idx = tid; idx < KI::CH; idx += 256) {
     const int c = idx / kBKV, r = idx % kBKV;
-    img[KI::KA + idx] = ld_vec<v8>(&krows[r][8 * c]);
-    img[KI::VA + idx] = ld_vec<v8>(&vrows[r][8 * c]);
+    const int at = c * kBKV + (r ^ (KI::SWZ * (c & 1)));
+    img[KI::KA + at] = ld_vec<v8>(&krows[r][8 * c]);
+    img[KI::VA + at] = ld_vec<v8>(&vrows[r][8 * c]);
   }
+  if constexpr (KI::HAS_T)
   for (int idx = tid; idx < KI::CH; idx += 256) {
     const int kc = idx / D, d = idx % D;
     const int r0 = 16 * (kc / 2);
@@ -564,8 +598,8 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + l32];
-        vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + l32];
+        kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + (l32 ^ (KI::SWZ * hi))];
+        vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + (l32 ^ (KI::SWZ * hi))];
       }
     } else {
 #pragma unroll
@@ -656,27 +690,8 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   f32x16 dv[MD], dk[MD];
 #pragma unroll
   for (int md = 0; md < MD; ++md) dv[md] = dk[md] = f32x16{};
-  // B's A operands (dO^T, q^T: lane l holds head-dim 32 md + l%32 over the 8
-  // rows that P's and dS's packed registers of its lane half give, kPermKey
-  // order: 16 half + 4 hi + {0..3, 8..11}) come from the row-major images by
-  // two ds_read_b64_tr_b16 each. That instruction hands lane j of a 16-lane
-  // group element j%4 of the 8-byte segments read by lanes j/4 + 4e, e = 0..3:
-  // lane s reads row 16 half + 8 k + 4 hi + s/4 at head-dim
-  // 32 md + 16 ((l/16)%2) + 4 (s%4), so lane j receives rows
-  // 16 half + 8 k + 4 hi + e at head-dim 32 md + l%32. Row r, head-dim d of
-  // an image sits at byte ((d/8)*32 + (r ^ 4*((d/8)%2)))*16 + (d%8)*2.
-  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const int tr_row = 4 * (hi ^ (QI::SWZ ? (tr_d >> 3) & 1 : 0)) + ((lane & 15) >> 2);  // column parity swizzle
-  const int tr_lane = ((tr_d >> 3) * kQRows + tr_row) * 16 + (tr_d & 7) * 2;
-  typedef short s4 __attribute__((ext_vector_type(4)));
-  auto tr_operand = [&](const unsigned char* img, int half, int md) {
-    const unsigned char* base = img + tr_lane + md * (4 * kQRows * 16) + half * 256;
-    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(base));
-    const s4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(base + 128));
-    typedef short s8 __attribute__((ext_vector_type(8)));
-    const s8 v = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(v8, v);
-  };
+  // B's A operands dO^T and q^T come out of the row-major images by
+  // transposing reads (tr_operand).
   walk([](int) {}, [&](int it) {
     if (it > 0) {
       const unsigned char* st = reinterpret_cast<const unsigned char*>(stage(it - 1));
@@ -689,7 +704,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
       prefetched_products<4 * MD, 8, v8>(
           [&](int j) {
             const int half = j / (2 * MD), md = (j >> 1) % MD;
-            return tr_operand(st + ((j & 1) ? QI::QA : QI::GA) * QI::CHB, half, md);
+            return tr_operand<v8>(st + ((j & 1) ? QI::QA : QI::GA) * QI::CHB, lane, half, md);
           },
           [&](int j, const v8& o) {
             const int half = j / (2 * MD), md = (j >> 1) % MD;
@@ -1162,7 +1177,7 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
       }
     if constexpr (QL > 0) {
       prefetched_products<2 * KS, QL, v8>(
-          [&](int j) { return st[((j & 1) ? KI::VA : KI::KA) + (2 * (j >> 1) + hi) * kBKV + l32]; },
+          [&](int j) { return st[((j & 1) ? KI::VA : KI::KA) + (2 * (j >> 1) + hi) * kBKV + (l32 ^ (KI::SWZ * hi))]; },
           [&](int j, const v8& o) {
             if (j & 1)
               dp[0] = mfma32(o, gf[j >> 1], dp[0]);
@@ -1174,8 +1189,8 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + l32], qf[ks], s[mt]);
-          dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + l32], gf[ks], dp[mt]);
+          s[mt] = mfma32(st[KI::KA + (2 * ks + hi) * kBKV + 32 * mt + (l32 ^ (KI::SWZ * hi))], qf[ks], s[mt]);
+          dp[mt] = mfma32(st[KI::VA + (2 * ks + hi) * kBKV + 32 * mt + (l32 ^ (KI::SWZ * hi))], gf[ks], dp[mt]);
         }
       lead_schedule<T, 2 * KS * MT, 4>();
     }
@@ -1203,14 +1218,21 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     // dQ^T += K^T dS^T
     if constexpr (QL > 0) {
       prefetched_products<KS2 * MD, QL, v8>(
-          [&](int j) { return st[KI::KT + (2 * (j / MD) + hi) * D + 32 * (j % MD) + l32]; },
+          [&](int j) {
+            if constexpr (KI::HAS_T)
+              return st[KI::KT + (2 * (j / MD) + hi) * D + 32 * (j % MD) + l32];
+            else
+              return tr_operand<v8>(reinterpret_cast<const unsigned char*>(st + KI::KA), lane, j / MD, j % MD);
+          },
           [&](int j, const v8& o) { dq[j % MD] = mfma32(o, dsf[j / MD], dq[j % MD]); });
     } else {
 #pragma unroll
       for (int ks2 = 0; ks2 < KS2; ++ks2)
 #pragma unroll
         for (int md = 0; md < MD; ++md)
-          dq[md] = mfma32(st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32], dsf[ks2], dq[md]);
+          dq[md] = mfma32(KI::HAS_T ? st[KI::KT + (2 * ks2 + hi) * D + 32 * md + l32]
+                                    : tr_operand<v8>(reinterpret_cast<const unsigned char*>(st + KI::KA), lane, ks2, md),
+                          dsf[ks2], dq[md]);
       lead_schedule<T, KS2 * MD, 4>();
     }
   };
