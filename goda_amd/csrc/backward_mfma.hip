@@ -11,15 +11,14 @@
 //      the row-major operand images of rotated q (prescaled) and of dO
 //      ("chunk-column-major" [D/8][32] 16-byte chunks, the A operand of a
 //      product over head_dim), plus the row statistics lse*log2(e) and
-//      delta; for the one-wave dk/dv kernel (head_dim 256, fp32) also the
-//      transposed images ([32/8][D] chunks with the rows of each 16-row
-//      group in kPermKey order, the A operand of a product over rows). The
-//      split dk/dv kernel reads those operands out of the row-major images
-//      with transposing LDS reads (ds_read_b64_tr_b16).
+//      delta; for fp32 also the transposed images ([32/8][D] chunks with the
+//      rows of each 16-row group in kPermKey order, the A operand of a
+//      product over rows). The 16-bit kernels read those operands out of the
+//      row-major images with transposing LDS reads (ds_read_b64_tr_b16).
 //   2. pack_kv_bwd_kernel: per (32-key tile, KV head, sequence), the
-//      row-major images of rotated k and of v and, for the one-wave kernels,
-//      the transposed image of k (the split path's dq reads k^T out of the
-//      row-major image with transposing LDS reads).
+//      row-major images of rotated k and of v and, for fp32, the transposed
+//      image of k (the 16-bit dq kernels read k^T out of the row-major image
+//      with transposing LDS reads).
 //   3. bwd_dkv_mfma_kernel: one workgroup of 8 waves per 128 keys of a KV
 //      head, in pairs (two waves of one SIMD) that share 32 keys; the pair
 //      pins the k and v operands of its keys and walks the query tiles of
@@ -68,14 +67,15 @@ struct DqShape {
 };
 
 // Images are counted in 8-element chunks (16 bytes, or 32 for fp32).
-// The transposed q and dO images (QT, GT) exist only where the one-wave dk/dv
-// kernel reads them (head_dim 256, fp32); the split dk/dv kernel reads its
-// transposed operands out of the row-major images with transposing LDS reads.
+// The transposed q and dO images (QT, GT) exist only for fp32 operands, which
+// have no transposing LDS read; the 16-bit dk/dv kernels read those operands
+// out of the row-major images (tr_operand). Without them the dK accumulators
+// multiply the prescaled q image: dk = ln(2) * dK^T (kDkScale).
 template <typename T, int D>
 struct QImg {
   static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);
   static constexpr int CH = D / 8 * kQRows;  // chunks of one image
-  static constexpr bool HAS_T = DqShape<T, D>::WIDE;
+  static constexpr bool HAS_T = sizeof(T) == 4;
   static constexpr int NIMG = HAS_T ? 4 : 2;
   static constexpr int QA = 0, GA = CH, QT = 2 * CH, GT = 3 * CH;
   // Row-major images: chunk (c, r) (head-dim 8c..8c+7 of row r) at
@@ -92,13 +92,21 @@ struct QImg {
 };
 
 // Key-side images: row-major k and v (with the query images' odd-column
-// swizzle) and, for the one-wave kernels only, the transposed k; the dq
-// kernel of the split path reads k^T out of the row-major image.
+// swizzle) and, for fp32 only, the transposed k; the 16-bit dq kernels read
+// k^T out of the row-major image.
+// Factor from the dK^T accumulators to dk: against the prescaled q image
+// (q * scale * log2(e)) it is ln(2), against the unscaled transposed image
+// the softmax scale.
+template <typename T, int D>
+__device__ __forceinline__ float dk_scale(const goda_prefill_args& a) {
+  return QImg<T, D>::HAS_T ? a.softmax_scale : kLn2;
+}
+
 template <typename T, int D>
 struct KVImg {
   static constexpr int CHB = (int)sizeof(typename Vec<T>::v8);
   static constexpr int CH = D / 8 * kBKV;
-  static constexpr bool HAS_T = DqShape<T, D>::WIDE;
+  static constexpr bool HAS_T = sizeof(T) == 4;
   static constexpr int NIMG = HAS_T ? 3 : 2;
   static constexpr int SWZ = HAS_T ? 0 : 4;
   static constexpr int KA = 0, VA = CH, KT = 2 * CH;
@@ -735,7 +743,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   // which holds q * scale * log2(e): dk = scale * (dS^T q) = ln(2) * dK^T.
 #pragma unroll
   for (int md = 0; md < MD / 2; ++md) {
-    f32x16 x1 = dk[md] * kLn2, x2 = dk[md + MD / 2] * kLn2;
+    f32x16 x1 = dk[md] * dk_scale<T, D>(a), x2 = dk[md + MD / 2] * dk_scale<T, D>(a);
     if (rot) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -780,9 +788,9 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
   constexpr int KS = D / 16;
   constexpr int MD = D / 32;
   constexpr int NTH = kWavesWide * 64;
-  constexpr int LOADS = 4 * QI::CH / NTH;
+  constexpr int LOADS = QI::NIMG * QI::CH / NTH;
   constexpr int PART = LOADS / kWideParts;
-  static_assert(4 * QI::CH % (NTH * kWideParts) == 0, "tile must split over the threads and parts");
+  static_assert(QI::NIMG * QI::CH % (NTH * kWideParts) == 0, "tile must split over the threads and parts");
   extern __shared__ __align__(16) unsigned char smem[];
 
   const goda_prefill_args& a = p.a;
@@ -808,8 +816,8 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     const v8* img = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, kw0 / kBKV, hk, p.ntk, a.heads_kv) * KI::BYTES);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + l32];
-      vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + l32];
+      kf[ks] = img[KI::KA + (2 * ks + hi) * kBKV + (l32 ^ (KI::SWZ * hi))];
+      vf[ks] = img[KI::VA + (2 * ks + hi) * kBKV + (l32 ^ (KI::SWZ * hi))];
     }
   } else {
 #pragma unroll
@@ -907,7 +915,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     // One wave per SIMD: nothing else hides a product's LDS operand latency,
     // so the reads run WL products ahead.
     prefetched_products<2 * KS, WL, v8>(
-        [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + l32]; },
+        [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + (l32 ^ (QI::SWZ * hi))]; },
         [&](int j, const v8& o) {
           if (j & 1)
             dp = mfma32(o, vf[j >> 1], dp);
@@ -944,13 +952,23 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     load_part(nsrc, 2);
     const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
     prefetched_products<2 * MD, WL, v8>(
-        [&](int j) { return st[QI::GT + (2 * (j & 1) + hi) * D + 32 * (j >> 1) + l32]; },
+        [&](int j) {
+          if constexpr (QI::HAS_T)
+            return st[QI::GT + (2 * (j & 1) + hi) * D + 32 * (j >> 1) + l32];
+          else
+            return tr_operand<v8>(reinterpret_cast<const unsigned char*>(st + QI::GA), lane, j & 1, j >> 1);
+        },
         [&](int j, const v8& o) { dv[j >> 1] = mfma32(o, (j & 1) ? pp1 : pp0, dv[j >> 1]); });
     store_next(2);
     load_part(nsrc, 3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
     prefetched_products<2 * MD, WL, v8>(
-        [&](int j) { return st[QI::QT + (2 * (j & 1) + hi) * D + 32 * (j >> 1) + l32]; },
+        [&](int j) {
+          if constexpr (QI::HAS_T)
+            return st[QI::QT + (2 * (j & 1) + hi) * D + 32 * (j >> 1) + l32];
+          else
+            return tr_operand<v8>(reinterpret_cast<const unsigned char*>(st + QI::QA), lane, j & 1, j >> 1);
+        },
         [&](int j, const v8& o) { dk[j >> 1] = mfma32(o, (j & 1) ? d1 : d0, dk[j >> 1]); });
     store_next(3);
     ring_barrier();
@@ -987,9 +1005,10 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
   const int pos = a.rope_k_offset + key;
   // dk: one pair of head-dim blocks (md, md + MD/2: the rotation's partners)
   // at a time, scaled and rotated back.
+  const float dks = dk_scale<T, D>(a);
 #pragma unroll
   for (int md = 0; md < MD / 2; ++md) {
-    f32x16 x1 = dk[md] * a.softmax_scale, x2 = dk[md + MD / 2] * a.softmax_scale;
+    f32x16 x1 = dk[md] * dks, x2 = dk[md + MD / 2] * dks;
     if (rot) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -1033,8 +1052,8 @@ __global__ void __launch_bounds__(256) bwd_dkv_reduce_kernel(const BwdParams p) 
     v1 += ld_vec<f32x4>(pv + d0);
     v2 += ld_vec<f32x4>(pv + d0 + D / 2);
   }
-  k1 *= a.softmax_scale;
-  k2 *= a.softmax_scale;
+  k1 *= dk_scale<T, D>(a);
+  k2 *= dk_scale<T, D>(a);
   if (a.rope_k && key < g.lk) {
     const int pos = a.rope_k_offset + key;
     const f32x4 cs = ld_vec<f32x4>(a.rope_cos + (int64_t)pos * (D / 2) + d0);
