@@ -43,8 +43,9 @@
 //        dP^T [keys][rows] = V dO^T        A = v image,   B = dO (registers)
 //        dQ^T [d][rows]   += K^T dS^T      A = K^T (image or transposing reads), B = dS^T (packed)
 // A packed accumulator becomes a B operand directly because the transposed
-// images hold their rows / keys in the accumulator's register order
-// (kPermKey). With the log-sum-exp known there is no online softmax.
+// operands (fp32 images, or transposing reads of the row-major images) hold
+// their rows / keys in the accumulator's register order (kPermKey). With the
+// log-sum-exp known there is no online softmax.
 
 #include <algorithm>
 
@@ -245,7 +246,7 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
   if (i0 >= g.lq) return;
   const bool varlen = a.cu_seqlens_q != nullptr;
   const int diag = g.lk - g.lq;
-  __shared__ __align__(16) T qrows[kQRows][D + 8];   // q for the transposed image (dK)
+  __shared__ __align__(16) T qrows[kQRows][D + 8];   // q for the transposed image (dK; fp32 only)
   __shared__ __align__(16) T qsrows[kQRows][D + 8];  // q * scale * log2(e) for the row-major one (S)
   __shared__ __align__(16) T grows[kQRows][D + 8];
   const int tid = threadIdx.x;
@@ -269,8 +270,10 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
     v8 qs1, qs2;
     norm_rope_row<T, D, HALF8>(q1, q2, c, a.q_norm_weight, a.norm_eps, i < g.lq && a.rope_q,
                                i < g.lq ? rope_qpos(a, diag, i) : 0, a, p.scale_log2, &qs1, &qs2);
-    st_vec<v8>(&qrows[r][c], q1);
-    st_vec<v8>(&qrows[r][c + D / 2], q2);
+    if constexpr (QI::HAS_T) {
+      st_vec<v8>(&qrows[r][c], q1);
+      st_vec<v8>(&qrows[r][c + D / 2], q2);
+    }
     st_vec<v8>(&qsrows[r][c], qs1);
     st_vec<v8>(&qsrows[r][c + D / 2], qs2);
     st_vec<v8>(&grows[r][c], g1);
