@@ -19,10 +19,11 @@
 //      belong to query heads of ONE KV head, so every K/V tile streamed into
 //      LDS serves the whole query-head group ("read once per group"). Tiles
 //      move through a ring of 4 LDS stages: during the interval that reads
-//      tiles j and j+1, each wave loads its share of tile j+3 into registers
-//      and writes it to a free stage (kStages below). (Direct global->LDS DMA
-//      would save those registers, but while such a load is in flight the
-//      compiler waits for ALL LDS reads before every MFMA operand use.)
+//      tiles j and j+1, each wave moves its share of tile j+3 into a free
+//      stage (kStages below), for 16-bit tiles by direct global->LDS loads
+//      (global_load_lds_dwordx4) issued from inline asm and waited for at the
+//      ring barrier (the compiler's own form of those loads makes it wait for
+//      them before every LDS operand read), for fp32 tiles through registers.
 //
 // Per wave and KV tile (32x32x16 MFMA, 32*NT query rows of one head):
 //   S^T[kv][q] = K'[kv][d] . Q^T[d][q] - m[q] + bias[kv][q]
@@ -518,6 +519,51 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     }
   };
   auto tile_store = [&](int j) { tile_store_part(j, SPLIT ? 1 : 0); };
+  // 16-bit tiles move by direct global->LDS loads instead: wave w's share of
+  // a tile is LOADS blocks of 64 consecutive 16-byte chunks, the same offsets
+  // in the workspace tile and in the LDS stage, and global_load_lds_dwordx4
+  // writes lane i's chunk at m0 + 16 i. Issued from inline asm, so the
+  // compiler neither counts them nor waits for them before LDS reads; the
+  // ring barrier waits for them instead (vmcnt(LOADS): every batch but the
+  // newest one complete). A tile lands in stage (j + kAhead) % kStages, which
+  // no wave reads between its issue (interval j, after the barrier) and the
+  // barrier opening interval j + kAhead - 1, where it is first read. (No
+  // other code in this file uses m0.)
+  constexpr bool DMA = sizeof(T) == 2;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // The instruction's immediate offset moves the global source and the LDS
+  // destination alike, so one m0 and one address serve a wave's whole share.
+  static_assert(!DMA || LOADS == 2 || LOADS == 4, "DMA share of 2 or 4 blocks");
+  // Scalar tile base plus a 32-bit per-lane offset (the instruction's saddr
+  // form): one loop-invariant VGPR.
+  const unsigned lane_off = (unsigned)((wave_u * LOADS * 64 + lane) * 16);
+  auto tile_dma = [&](int j) {
+    const unsigned long long base =
+        (unsigned long long)(uintptr_t)(ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES);
+    const unsigned lds0 =
+        (unsigned)(uintptr_t)(smem + (j % kStages) * TG::BYTES) + (unsigned)(wave_u * LOADS * 64 * 16);
+    if constexpr (LOADS == 2)
+      asm volatile(
+          "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2\n\tglobal_load_lds_dwordx4 %1, %2 offset:1024"
+          :
+          : "s"(lds0), "v"(lane_off), "s"(base)
+          : "memory");
+    else
+      asm volatile(
+          "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2\n\tglobal_load_lds_dwordx4 %1, %2 offset:1024\n\t"
+          "global_load_lds_dwordx4 %1, %2 offset:2048\n\tglobal_load_lds_dwordx4 %1, %2 offset:3072"
+          :
+          : "s"(lds0), "v"(lane_off), "s"(base)
+          : "memory");
+  };
+  auto dma_barrier = [&]() {
+    if constexpr (LOADS == 2)
+      asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (LOADS == 4)
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
 
   // This lane's K' operand for (ks, mt) is chunk (2ks + hi)*BKV + 32mt + l32;
   // its V^T operand for (ks2, md) is chunk (2ks2 + hi)*D + 32md + l32.
@@ -702,11 +748,16 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // tile j + kAhead (its global loads are issued now, its LDS stores go out
   // mid-interval and at the end).
   auto ring_begin = [&](int j) {
+    if constexpr (DMA) {
+      dma_barrier();
+      if (j + kAhead < j_hi) tile_dma(j + kAhead);
+      return;
+    }
     if ((j - j_lo) % kBarrierEvery == kBarrierEvery - 1) ring_barrier();  // the prologue's barrier opens interval j_lo
     if (j + kAhead < j_hi) tile_load_part(j + kAhead, 0);
   };
   auto ring_mid = [&](int j) {
-    if constexpr (SPLIT) {
+    if constexpr (SPLIT && !DMA) {
       if (j + kAhead < j_hi) {
         tile_store_part(j + kAhead, 0);
         tile_load_part(j + kAhead, 1);
@@ -714,7 +765,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     }
   };
   auto ring_end = [&](int j) {
-    if (j + kAhead < j_hi) tile_store(j + kAhead);
+    if constexpr (!DMA)
+      if (j + kAhead < j_hi) tile_store(j + kAhead);
   };
 
   // ---- prologue: tiles j_lo .. j_lo + kAhead - 1 resident, scores of tile j_lo --------
@@ -722,9 +774,14 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   f32x16 s_a[MT][NT];
   v8 pf[NT][KS2];
   if (ntile > 0) {
-    for (int t = 0; t < kAhead && t < ntile; ++t) {
-      tile_load(j_lo + t);
-      tile_store(j_lo + t);
+    if constexpr (DMA) {
+      for (int t = 0; t < kAhead && t < ntile; ++t) tile_dma(j_lo + t);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      for (int t = 0; t < kAhead && t < ntile; ++t) {
+        tile_load(j_lo + t);
+        tile_store(j_lo + t);
+      }
     }
     ring_barrier();
     qk(j_lo, s_a);
