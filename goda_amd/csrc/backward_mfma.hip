@@ -566,41 +566,43 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   const int nq = i_hi > i_lo ? (i_hi - 1) / kQRows + 1 - qt_lo : 0;
   const int n = p.group * nq;
 
-  v8 stg[LOADS];
-  v8 stg_stat;
-  QWalkDown ld(0, nq, p.group);  // the next tile to load; loads come in walk order
-  auto tile_load = [&]() {
+  // Query tiles move into the ring by direct global->LDS loads (dma_blocks),
+  // issued by the B waves only (A's scores are the critical path): B wave w's
+  // share of a tile is 2 LOADS blocks of 64 consecutive 16-byte chunks at
+  // the same offsets in the image and in the stage, and wave 4's lanes below
+  // STAT_CH copy the row statistics. Tile it + 1 lands in stage
+  // (it + 1) % kKvStages during interval it, when A reads stage it % kKvStages
+  // and B stage (it - 1) % kKvStages; the barrier opening interval it + 1
+  // waits for it (vmcnt(0)).
+  static_assert(2 * LOADS == 2 || 2 * LOADS == 4, "DMA share of 2 or 4 blocks");
+  static_assert(QI::STAT_CH <= 64, "statistics fit one wave's copy");
+  const int bw = __builtin_amdgcn_readfirstlane(wave) & 3;
+  const unsigned lane_off = (unsigned)((bw * 2 * LOADS * 64 + lane) * 16);
+  const unsigned stat_off = (unsigned)((QI::STAT + lane) * 16);
+  QWalkDown ld(0, nq, p.group);  // the next tile to copy; copies come in walk order
+  auto tile_dma = [&](int it) {
     const int64_t t = q_tile_index(b, qt_lo + ld.q, hk * p.group + ld.h, p.ntq, a.heads_q);
-    const v8* src = reinterpret_cast<const v8*>(p.qimg + t * QI::BYTES);
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) stg[i] = src[tid + i * kWavesKv * 64];
-    if (tid < QI::STAT_CH) stg_stat = src[QI::STAT + tid];
     ld.next();
-  };
-  auto tile_store = [&](int it) {
-    v8* dst = reinterpret_cast<v8*>(smem + (it % kKvStages) * QI::BYTES);
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) dst[tid + i * kWavesKv * 64] = stg[i];
-    if (tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
+    const unsigned long long base = (unsigned long long)(uintptr_t)(p.qimg + t * QI::BYTES);
+    const unsigned lds = (unsigned)(uintptr_t)(smem + (it % kKvStages) * QI::BYTES);
+    dma_blocks<2 * LOADS>(lds + (unsigned)(bw * 2 * LOADS * 64 * 16), lane_off, base);
+    if (bw == 0 && lane < QI::STAT_CH) dma_blocks<1>(lds + QI::STAT * 16, stat_off, base);
   };
   auto stage = [&](int it) { return reinterpret_cast<const v8*>(smem + (it % kKvStages) * QI::BYTES); };
   auto xchg = [&](int it, int c) -> v8& { return xbuf[(((it & 1) * 4 + pair) * 4 + c) * 64 + lane]; };
   // Iterations 0..n of a role (B runs one tile behind A, so both take n + 1
-  // barriers). `pre(it)` issues the role's own global loads ahead of the
-  // tile loads (the load counter drains in order).
-  auto walk = [&](auto&& pre, auto&& step) {
-    if (n > 0) {
-      tile_load();
-      tile_store(0);
-    }
+  // barriers). `pre(it)` issues the role's own global loads; `copy(it)` the
+  // tile copies of the role that makes them.
+  auto walk = [&](auto&& copy, auto&& pre, auto&& step) {
+    if (n > 0) copy(0);
     for (int it = 0; it <= n; ++it) {
-      ring_barrier();
+      dma_ring_barrier<0>();
+      if (it + 1 < n) copy(it + 1);
       pre(it);
-      if (it + 1 < n) tile_load();
       step(it);
-      if (it + 1 < n) tile_store(it + 1);
     }
   };
+  auto no_copy = [](int) {};
 
   if (!role_b) {
     // ---- A: scores --------------------------------------------------------
@@ -630,7 +632,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         mword = p.mask_t[b * p.mt_stride_b + (hk * p.group + cu.h) * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo +
                          cu.q] >> (4 * hi);
     };
-    walk(pre, [&](int it) {
+    walk(no_copy, pre, [&](int it) {
       if (it < n) {
         const int hq = hk * p.group + cu.h;
         const int q0 = (qt_lo + cu.q) * kQRows;
@@ -703,7 +705,7 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   for (int md = 0; md < MD; ++md) dv[md] = dk[md] = f32x16{};
   // B's A operands dO^T and q^T come out of the row-major images by
   // transposing reads (tr_operand).
-  walk([](int) {}, [&](int it) {
+  walk(tile_dma, [](int) {}, [&](int it) {
     if (it > 0) {
       const unsigned char* st = reinterpret_cast<const unsigned char*>(stage(it - 1));
       const v8 p0 = xchg(it - 1, 0), p1 = xchg(it - 1, 1);

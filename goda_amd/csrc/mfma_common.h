@@ -37,6 +37,48 @@ constexpr int kMfmaPerStep = sizeof(T) == 4 ? 8 : 1;
 // registers directly, with no register shuffles.
 __host__ __device__ constexpr int kPermKey(int p) { return 8 * ((p % 8) / 4) + 4 * (p / 8) + p % 4; }
 
+// Direct global->LDS copy by one wave of N (1, 2 or 4) consecutive 1 KB
+// blocks: lane i's 16 bytes of block k go from base + lane_off + 1024 k to
+// LDS byte address lds + 16 i + 1024 k (global_load_lds_dwordx4 writes lane
+// i's data at m0 + 16 i, and its immediate offset moves the global source and
+// the LDS destination alike; both checked in bounds on the GPU). Lanes
+// outside EXEC copy nothing. Issued from inline asm, so the compiler neither
+// counts these loads nor makes LDS reads wait for them: the caller waits
+// (vmcnt) before the barrier that publishes the data. Sets m0, which no code
+// of these kernels otherwise uses.
+template <int N>
+__device__ __forceinline__ void dma_blocks(unsigned lds, unsigned lane_off, unsigned long long base) {
+  static_assert(N == 1 || N == 2 || N == 4, "1, 2 or 4 blocks");
+  if constexpr (N == 1)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" : : "s"(lds), "v"(lane_off), "s"(base) : "memory");
+  else if constexpr (N == 2)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2\n\tglobal_load_lds_dwordx4 %1, %2 offset:1024"
+                 :
+                 : "s"(lds), "v"(lane_off), "s"(base)
+                 : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2\n\tglobal_load_lds_dwordx4 %1, %2 offset:1024\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:2048\n\tglobal_load_lds_dwordx4 %1, %2 offset:3072"
+        :
+        : "s"(lds), "v"(lane_off), "s"(base)
+        : "memory");
+}
+
+// The tile rings' barrier when their tiles arrive by dma_blocks: this wave's
+// copies have landed (vmcnt(N): all but its N most recent loads), then the
+// workgroup barrier makes every wave's copies visible.
+template <int N>
+__device__ __forceinline__ void dma_ring_barrier() {
+  static_assert(N == 0 || N == 2 || N == 4, "0, 2 or 4 loads in flight");
+  if constexpr (N == 0)
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 2)
+    asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Workgroup barrier for the tile rings. __syncthreads() would also wait for
 // every outstanding global access (vmcnt(0)), i.e. for the registers of the
 // tile being prefetched; a ring only needs this wave's LDS accesses retired.

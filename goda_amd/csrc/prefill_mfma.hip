@@ -519,51 +519,25 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     }
   };
   auto tile_store = [&](int j) { tile_store_part(j, SPLIT ? 1 : 0); };
-  // 16-bit tiles move by direct global->LDS loads instead: wave w's share of
-  // a tile is LOADS blocks of 64 consecutive 16-byte chunks, the same offsets
-  // in the workspace tile and in the LDS stage, and global_load_lds_dwordx4
-  // writes lane i's chunk at m0 + 16 i. Issued from inline asm, so the
-  // compiler neither counts them nor waits for them before LDS reads; the
-  // ring barrier waits for them instead (vmcnt(LOADS): every batch but the
-  // newest one complete). A tile lands in stage (j + kAhead) % kStages, which
-  // no wave reads between its issue (interval j, after the barrier) and the
-  // barrier opening interval j + kAhead - 1, where it is first read. (No
-  // other code in this file uses m0.)
+  // 16-bit tiles move by direct global->LDS loads instead (dma_blocks): wave
+  // w's share of a tile is LOADS blocks of 64 consecutive 16-byte chunks, the
+  // same offsets in the workspace tile and in the LDS stage. The ring barrier
+  // waits vmcnt(LOADS): every batch but the newest one has landed. A tile
+  // lands in stage (j + kAhead) % kStages, which no wave reads between its
+  // issue (interval j, after the barrier) and the barrier opening interval
+  // j + kAhead - 1, where it is first read.
   constexpr bool DMA = sizeof(T) == 2;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  // The instruction's immediate offset moves the global source and the LDS
-  // destination alike, so one m0 and one address serve a wave's whole share.
   static_assert(!DMA || LOADS == 2 || LOADS == 4, "DMA share of 2 or 4 blocks");
-  // Scalar tile base plus a 32-bit per-lane offset (the instruction's saddr
-  // form): one loop-invariant VGPR.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const unsigned lane_off = (unsigned)((wave_u * LOADS * 64 + lane) * 16);
   auto tile_dma = [&](int j) {
     const unsigned long long base =
         (unsigned long long)(uintptr_t)(ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES);
     const unsigned lds0 =
         (unsigned)(uintptr_t)(smem + (j % kStages) * TG::BYTES) + (unsigned)(wave_u * LOADS * 64 * 16);
-    if constexpr (LOADS == 2)
-      asm volatile(
-          "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2\n\tglobal_load_lds_dwordx4 %1, %2 offset:1024"
-          :
-          : "s"(lds0), "v"(lane_off), "s"(base)
-          : "memory");
-    else
-      asm volatile(
-          "s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2\n\tglobal_load_lds_dwordx4 %1, %2 offset:1024\n\t"
-          "global_load_lds_dwordx4 %1, %2 offset:2048\n\tglobal_load_lds_dwordx4 %1, %2 offset:3072"
-          :
-          : "s"(lds0), "v"(lane_off), "s"(base)
-          : "memory");
+    dma_blocks<LOADS>(lds0, lane_off, base);
   };
-  auto dma_barrier = [&]() {
-    if constexpr (LOADS == 2)
-      asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (LOADS == 4)
-      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  };
+  auto dma_barrier = [&]() { dma_ring_barrier<LOADS>(); };
 
   // This lane's K' operand for (ks, mt) is chunk (2ks + hi)*BKV + 32mt + l32;
   // its V^T operand for (ks2, md) is chunk (2ks2 + hi)*D + 32md + l32.
