@@ -867,16 +867,41 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
   };
 
+  // 16-bit tiles move by direct global->LDS loads instead (dma_span): wave w
+  // copies chunks [w LOADS 64, (w + 1) LOADS 64) of the image to the same
+  // offsets of the stage, and wave 0's lanes below STAT_CH the statistics.
+  // Tile it + 1 lands in stage (it + 1) % 2 during interval it (the barrier
+  // opening the interval ends every read of tile it - 1 there); the barrier
+  // closing the interval waits for the copies (vmcnt(0)). fp32 images
+  // (32-byte chunks) are staged through registers, in parts between the
+  // product phases.
+  constexpr bool DMA = sizeof(T) == 2;
+  static_assert(QI::STAT_CH <= 64, "statistics fit one wave's copy");
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const unsigned lane_off = (unsigned)((wave_u * LOADS * 64 + lane) * 16);
+  const unsigned stat_off = (unsigned)((QI::STAT + lane) * 16);
+  auto tile_dma = [&](const QWalk& w, int it) {
+    const unsigned long long base = (unsigned long long)(uintptr_t)src_of(w);
+    const unsigned lds = (unsigned)(uintptr_t)(smem + (it % 2) * QI::BYTES);
+    dma_span<DMA ? LOADS : 1>(lds + (unsigned)(wave_u * LOADS * 64 * 16), lane_off, base);
+    if (wave_u == 0 && lane < QI::STAT_CH) dma_blocks<1>(lds + QI::STAT * 16, stat_off, base);
+  };
+
   QWalk cu(it0, nq), nw(it0, nq);
-  if (it0 < it1) {
-    const v8* src = src_of(cu);
+  if constexpr (DMA) {
+    if (it0 < it1) tile_dma(cu, it0);
+    dma_ring_barrier<0>();
+  } else {
+    if (it0 < it1) {
+      const v8* src = src_of(cu);
 #pragma unroll
-    for (int part = 0; part < kWideParts; ++part) {
-      load_part(src, part);
-      store_part(it0, part);
+      for (int part = 0; part < kWideParts; ++part) {
+        load_part(src, part);
+        store_part(it0, part);
+      }
     }
+    ring_barrier();
   }
-  ring_barrier();
   for (int it = it0; it < it1; ++it) {
     // The next tile is staged into the other stage (on the last tile: this
     // tile again, into a stage nobody reads), so the loop body is branch-free.
@@ -890,13 +915,21 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
     const v8* st = reinterpret_cast<const v8*>(smem + (it % 2) * QI::BYTES);
     const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
     auto store_next = [&](int part) {
-      v8* dst = reinterpret_cast<v8*>(smem + ((it + 1) % 2) * QI::BYTES);
+      if constexpr (!DMA) {
+        v8* dst = reinterpret_cast<v8*>(smem + ((it + 1) % 2) * QI::BYTES);
 #pragma unroll
-      for (int i = 0; i < PART; ++i) dst[tid + (part * PART + i) * NTH] = stg[i];
-      if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
+        for (int i = 0; i < PART; ++i) dst[tid + (part * PART + i) * NTH] = stg[i];
+        if (part == 0 && tid < QI::STAT_CH) dst[QI::STAT + tid] = stg_stat;
+      }
+    };
+    auto next_part = [&](int part) {
+      if constexpr (!DMA) load_part(nsrc, part);
     };
 
-    load_part(nsrc, 0);
+    if constexpr (DMA) {
+      if (it + 1 < it1) tile_dma(nw, it + 1);
+    }
+    next_part(0);
     // The caller's mask bits of this key for the tile's 32 rows.
     uint32_t mword = 0;
     if (MASK && key < g.lk)
@@ -928,7 +961,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
             s = mfma32(o, kf[j >> 1], s);
         });
     store_next(0);
-    load_part(nsrc, 1);
+    next_part(1);
 
     // P and dS; visibility as a range of the register's row offset.
     int lo_lim = -1, hi_lim = g.lq - 1 - rel;
@@ -954,7 +987,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
       }
     }
     store_next(1);
-    load_part(nsrc, 2);
+    next_part(2);
     const v8 pp0 = pack8<v8, T>(pr), pp1 = pack8<v8, T>(pr + 8);
     prefetched_products<2 * MD, WL, v8>(
         [&](int j) {
@@ -965,7 +998,7 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
         },
         [&](int j, const v8& o) { dv[j >> 1] = mfma32(o, (j & 1) ? pp1 : pp0, dv[j >> 1]); });
     store_next(2);
-    load_part(nsrc, 3);
+    next_part(3);
     const v8 d0 = pack8<v8, T>(ds), d1 = pack8<v8, T>(ds + 8);
     prefetched_products<2 * MD, WL, v8>(
         [&](int j) {
@@ -976,7 +1009,10 @@ __global__ void __launch_bounds__(kWavesWide * 64, 1) bwd_dkv_wide_kernel(const 
         },
         [&](int j, const v8& o) { dk[j >> 1] = mfma32(o, (j & 1) ? d1 : d0, dk[j >> 1]); });
     store_next(3);
-    ring_barrier();
+    if constexpr (DMA)
+      dma_ring_barrier<0>();
+    else
+      ring_barrier();
   }
 
   // ---- epilogue: lane l32 owns key row `key`; register (md, r) is head-dim
@@ -1166,7 +1202,20 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
 #pragma unroll
   for (int md = 0; md < MD; ++md) dq[md] = f32x16{};
 
-  v8 stg[LOADS];
+  // 16-bit tiles move by direct global->LDS loads (dma_span): wave w copies
+  // chunks [w LOADS 64, (w + 1) LOADS 64) of the image to the same offsets
+  // of the stage. fp32 images (32-byte chunks) are staged through registers.
+  constexpr bool DMA = sizeof(T) == 2;
+  static_assert(!DMA || KI::CHUNKS % (kWavesDq * 64) == 0, "16-bit tile splits over the waves");
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const unsigned lane_off = (unsigned)((wave_u * LOADS * 64 + lane) * 16);
+  auto tile_dma = [&](int it) {
+    const unsigned long long base =
+        (unsigned long long)(uintptr_t)(p.kvimg + kv_tile_index(b, j_lo + it, hk, p.ntk, a.heads_kv) * KI::BYTES);
+    const unsigned lds = (unsigned)(uintptr_t)(smem + (it % 2) * KI::BYTES) + (unsigned)(wave_u * LOADS * 64 * 16);
+    dma_span<DMA ? LOADS : 1>(lds, lane_off, base);
+  };
+  v8 stg[DMA ? 1 : LOADS];
   auto tile_load = [&](int it) {
     const v8* src = reinterpret_cast<const v8*>(p.kvimg + kv_tile_index(b, j_lo + it, hk, p.ntk, a.heads_kv) * KI::BYTES);
 #pragma unroll
@@ -1261,16 +1310,28 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     }
   };
 
-  if (n > 0) {
-    tile_load(0);
-    tile_store(0);
-  }
-  ring_barrier();
-  for (int it = 0; it < n; ++it) {
-    if (it + 1 < n) tile_load(it + 1);
-    compute(it);
-    if (it + 1 < n) tile_store(it + 1);
+  if constexpr (DMA) {
+    // Tile it + 1 lands in stage (it + 1) % 2 during interval it: the
+    // barrier opening the interval ends every read of tile it - 1 there, and
+    // the one opening interval it + 1 waits for the copies (vmcnt(0)).
+    if (n > 0) tile_dma(0);
+    for (int it = 0; it < n; ++it) {
+      dma_ring_barrier<0>();
+      if (it + 1 < n) tile_dma(it + 1);
+      compute(it);
+    }
+  } else {
+    if (n > 0) {
+      tile_load(0);
+      tile_store(0);
+    }
     ring_barrier();
+    for (int it = 0; it < n; ++it) {
+      if (it + 1 < n) tile_load(it + 1);
+      compute(it);
+      if (it + 1 < n) tile_store(it + 1);
+      ring_barrier();
+    }
   }
 
   // ---- epilogue: lane l32 owns query row i; register (md, r) is head-dim

@@ -49,6 +49,15 @@ __host__ __device__ constexpr int kPermKey(int p) { return 8 * ((p % 8) / 4) + 4
 template <int N>
 __device__ __forceinline__ void dma_blocks(unsigned lds, unsigned lane_off, unsigned long long base) {
   static_assert(N == 1 || N == 2 || N == 4, "1, 2 or 4 blocks");
+  // Both are wave-uniform; readfirstlane keeps them in scalar registers where
+  // the compiler would otherwise hand the "s" operands a VGPR copy (it costs
+  // nothing for a value already in SGPRs).
+  // (The builtin is 32-bit and returns int: each half goes back through
+  // unsigned, so the low half is not sign-extended into the high one.)
+  lds = (unsigned)__builtin_amdgcn_readfirstlane(lds);
+  const unsigned base_hi = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(base >> 32));
+  const unsigned base_lo = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)base);
+  base = ((unsigned long long)base_hi << 32) | base_lo;
   if constexpr (N == 1)
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" : : "s"(lds), "v"(lane_off), "s"(base) : "memory");
   else if constexpr (N == 2)
@@ -63,6 +72,19 @@ __device__ __forceinline__ void dma_blocks(unsigned lds, unsigned lane_off, unsi
         :
         : "s"(lds), "v"(lane_off), "s"(base)
         : "memory");
+}
+
+// N blocks (N = 1, 2, or a multiple of 4) as dma_blocks calls of at most 4
+// (the immediate offset reaches 4095 bytes).
+template <int N>
+__device__ __forceinline__ void dma_span(unsigned lds, unsigned lane_off, unsigned long long base) {
+  if constexpr (N <= 4) {
+    dma_blocks<N>(lds, lane_off, base);
+  } else {
+    static_assert(N % 4 == 0, "spans beyond 4 blocks come in 4s");
+    dma_blocks<4>(lds, lane_off, base);
+    dma_span<N - 4>(lds + 4096, lane_off, base + 4096);
+  }
 }
 
 // The tile rings' barrier when their tiles arrive by dma_blocks: this wave's
