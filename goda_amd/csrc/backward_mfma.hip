@@ -429,8 +429,10 @@ __global__ void __launch_bounds__(256) bwd_mask_t_kernel(const BwdParams p) {
 // the operand L products later, and scheduling fences keep that order (left
 // alone, the compiler moves every read next to its product, leaving about one
 // in flight; `lead_schedule` asks for the order but is not always honoured).
-template <int NJ, int L, typename V, typename Src, typename Prod>
-__device__ __forceinline__ void prefetched_products(Src src, Prod prod) {
+// `after(j)` runs after product j, inside the same fence: independent VALU
+// work placed there issues while the products execute.
+template <int NJ, int L, typename V, typename Src, typename Prod, typename After>
+__device__ __forceinline__ void prefetched_products(Src src, Prod prod, After after) {
   constexpr int P = L < NJ ? L : NJ;
   V op[P];
 #pragma unroll
@@ -440,8 +442,14 @@ __device__ __forceinline__ void prefetched_products(Src src, Prod prod) {
   for (int j = 0; j < NJ; ++j) {
     prod(j, op[j % P]);
     if (j + P < NJ) op[j % P] = src(j + P);
+    after(j);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+template <int NJ, int L, typename V, typename Src, typename Prod>
+__device__ __forceinline__ void prefetched_products(Src src, Prod prod) {
+  prefetched_products<NJ, L, V>(src, prod, [](int) {});
 }
 
 // Schedule of a phase of NM MFMAs, each with one LDS operand read: the reads
@@ -477,13 +485,17 @@ __device__ __forceinline__ V pack8(const float* x) {
 // hands both, packed as operands, to its partner through LDS. Wave w + 4
 // ("B", gradients, same SIMD) holds the dV^T and dK^T accumulators and, one
 // tile behind, issues dV^T += dO^T P and dK^T += Q^T dS. Each iteration
-// starts with the matrix products of both waves and ends with A's VALU work:
-// a wave's VALU instructions do not issue while the other wave of its SIMD
-// has matrix instructions waiting, so no VALU work sits between B's products.
-// Query tiles move through a three-stage ring (A reads tile it, B tile it-1,
-// tile it+1 is being stored); the P / dS exchange is double-buffered.
+// A wave's VALU instructions do not issue while the other wave of its SIMD
+// has matrix instructions waiting, so A's VALU work cannot hide under B's
+// products: A runs one tile ahead of itself instead, issuing the products of
+// tile it + 1 with the VALU work of tile it (P, dS) placed between them, where
+// it issues while A's own products execute. Query tiles move through a
+// four-stage ring (A reads tiles it and it + 1, B tile it - 1, tile it + 2 is
+// being copied); the P / dS exchange is double-buffered. (Copying two tiles
+// ahead through a fifth stage is slower: the copies then land during the
+// products, whose operand reads already saturate the LDS.)
 constexpr int kWavesKv = 8;
-constexpr int kKvStages = 3;
+constexpr int kKvStages = 4;
 
 template <typename T, int D>
 struct DkvSmem {
@@ -570,10 +582,10 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   // issued by the B waves only (A's scores are the critical path): B wave w's
   // share of a tile is 2 LOADS blocks of 64 consecutive 16-byte chunks at
   // the same offsets in the image and in the stage, and wave 4's lanes below
-  // STAT_CH copy the row statistics. Tile it + 1 lands in stage
-  // (it + 1) % kKvStages during interval it, when A reads stage it % kKvStages
-  // and B stage (it - 1) % kKvStages; the barrier opening interval it + 1
-  // waits for it (vmcnt(0)).
+  // STAT_CH copy the row statistics. Tile it + 2 lands in stage
+  // (it + 2) % kKvStages during interval it, when A reads stages it and
+  // it + 1 and B stage it - 1 (all mod kKvStages); the barrier opening
+  // interval it + 1 waits for it (vmcnt(0)).
   static_assert(2 * LOADS == 2 || 2 * LOADS == 4, "DMA share of 2 or 4 blocks");
   static_assert(QI::STAT_CH <= 64, "statistics fit one wave's copy");
   const int bw = __builtin_amdgcn_readfirstlane(wave) & 3;
@@ -595,14 +607,29 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
   // tile copies of the role that makes them.
   auto walk = [&](auto&& copy, auto&& pre, auto&& step) {
     if (n > 0) copy(0);
+    if (n > 1) copy(1);
     for (int it = 0; it <= n; ++it) {
       dma_ring_barrier<0>();
-      if (it + 1 < n) copy(it + 1);
+      if (it + 2 < n) copy(it + 2);
       pre(it);
       step(it);
     }
   };
-  auto no_copy = [](int) {};
+  // The same intervals unrolled by two: `step(it, parity)` gets the parity as
+  // a compile-time constant, so A's two accumulator sets keep fixed registers.
+  auto walk2 = [&](auto&& pre, auto&& step) {
+    auto interval = [&](int it, auto parity) {
+      dma_ring_barrier<0>();
+      pre(it);
+      step(it, parity);
+    };
+    for (int it = 0;; it += 2) {
+      interval(it, std::integral_constant<int, 0>{});
+      if (it + 1 > n) break;
+      interval(it + 1, std::integral_constant<int, 1>{});
+      if (it + 2 > n) break;
+    }
+  };
 
   if (!role_b) {
     // ---- A: scores --------------------------------------------------------
@@ -632,68 +659,90 @@ __global__ void __launch_bounds__(kWavesKv * 64, 1) bwd_dkv_mfma_kernel(const Bw
         mword = p.mask_t[b * p.mt_stride_b + (hk * p.group + cu.h) * p.mt_stride_h + (int64_t)key * p.ntq + qt_lo +
                          cu.q] >> (4 * hi);
     };
-    walk(no_copy, pre, [&](int it) {
-      if (it < n) {
-        const int hq = hk * p.group + cu.h;
-        const int q0 = (qt_lo + cu.q) * kQRows;
-        cu.next();
-        const v8* st = stage(it);
-        const float* stat = reinterpret_cast<const float*>(st + QI::STAT);
-        // S [rows][keys] and dP: two interleaved accumulation chains (the q
-        // image holds q * scale * log2(e): S leaves the matrix core in log2
-        // units).
-        f32x16 s = f32x16{}, dp = f32x16{};
-        prefetched_products<2 * KS, 4, v8>(
-            [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + (l32 ^ (QI::SWZ * hi))]; },
-            [&](int j, const v8& o) {
-              if (j & 1)
-                dp = mfma32(o, vf[j >> 1], dp);
-              else
-                s = mfma32(o, kf[j >> 1], s);
-            });
-        // P and dS; visibility as a range of the register's row offset
-        // off = row - (q0 + 4 hi). (Starting the accumulators at -lse2 and
-        // -delta, as the head_dim-256 and dq kernels do, saves two VALU
-        // instructions per entry but makes the products wait for the row
-        // statistics' LDS reads: 2% slower here.)
-        const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
-        const int rel = q0 + 4 * hi;
-        int lo_lim = -1, hi_lim = g.lq - 1 - rel;
-        if (a.causal) lo_lim = key - diag - rel;
-        if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
-        // Visible rows as one bit per register offset (bit off = 8 gq + e).
-        uint32_t vis = key_ok ? range_bits(lo_lim, hi_lim) : 0u;
-        if (MASK) vis &= mword;
-        const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
-        float pr[16], ds[16];
+    // S [rows][keys] and dP of tile `it` into (sn, dpn): two interleaved
+    // accumulation chains (the q image holds q * scale * log2(e): S leaves
+    // the matrix core in log2 units); after(j) follows product j.
+    auto products = [&](int it, f32x16& sn, f32x16& dpn, auto&& after) {
+      const v8* st = stage(it);
+      sn = f32x16{};
+      dpn = f32x16{};
+      prefetched_products<2 * KS, 4, v8>(
+          [&](int j) { return st[((j & 1) ? QI::GA : QI::QA) + (2 * (j >> 1) + hi) * kQRows + (l32 ^ (QI::SWZ * hi))]; },
+          [&](int j, const v8& o) {
+            if (j & 1)
+              dpn = mfma32(o, vf[j >> 1], dpn);
+            else
+              sn = mfma32(o, kf[j >> 1], sn);
+          },
+          after);
+    };
+    // P and dS of tile it from (s, dp), interleaved with the products of tile
+    // it + 1 into (sn, dpn); RPS registers after each product.
+    constexpr int RPS = 16 / (2 * KS);
+    static_assert(16 % (2 * KS) == 0, "whole registers per product");
+    auto scores = [&](int it, const f32x16& s, const f32x16& dp, f32x16& sn, f32x16& dpn) {
+      const int hq = hk * p.group + cu.h;
+      const int q0 = (qt_lo + cu.q) * kQRows;
+      cu.next();
+      const float* stat = reinterpret_cast<const float*>(stage(it) + QI::STAT);
+      f32x4 l2[4], dl[4];
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const f32x4 l2 = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
-          const f32x4 dl = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+      for (int gq = 0; gq < 4; ++gq) {
+        l2[gq] = ld_vec<f32x4>(stat + 8 * gq + 4 * hi);
+        dl[gq] = ld_vec<f32x4>(stat + kQRows + 8 * gq + 4 * hi);
+      }
+      // Visibility as a range of the register's row offset
+      // off = row - (q0 + 4 hi). (Starting the accumulators at -lse2 and
+      // -delta, as the head_dim-256 and dq kernels do, saves two VALU
+      // instructions per entry but makes the products wait for the row
+      // statistics' LDS reads.)
+      const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
+      const int rel = q0 + 4 * hi;
+      int lo_lim = -1, hi_lim = g.lq - 1 - rel;
+      if (a.causal) lo_lim = key - diag - rel;
+      if (use_window) hi_lim = min(hi_lim, key + a.window_left - diag - rel);
+      // Visible rows as one bit per register offset (bit off = 8 gq + e).
+      uint32_t vis = key_ok ? range_bits(lo_lim, hi_lim) : 0u;
+      if (MASK) vis &= mword;
+      const float base = ALIBI ? slope2 * (float)(key - diag - rel) : 0.f;
+      float pr[16], ds[16];
+      auto slice = [&](int j) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * gq + e;
-            float t = s[r];
-            if (ALIBI) t += base - slope2 * (float)(8 * gq + e);
-            pr[r] = fast_exp2(t - l2[e]);
-            ds[r] = pr[r] * (dp[r] - dl[e]);
-          }
+        for (int k = 0; k < RPS; ++k) {
+          const int r = j * RPS + k, gq = r >> 2, e = r & 3;
+          float t = s[r];
+          if (ALIBI) t += base - slope2 * (float)(8 * gq + e);
+          pr[r] = fast_exp2(t - l2[gq][e]);
+          ds[r] = pr[r] * (dp[r] - dl[gq][e]);
         }
-        // Hidden entries are replaced (not scaled: exp2 of a hidden score
-        // may overflow) on the tiles where some lane of the wave has one; a
-        // wave-uniform branch, most tiles skip it.
-        if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
+      };
+      // (On the last tile the products re-read tile it; they go unused.)
+      products(min(it + 1, n - 1), sn, dpn, slice);
+      // Hidden entries are replaced (not scaled: exp2 of a hidden score may
+      // overflow) on the tiles where some lane of the wave has one; a
+      // wave-uniform branch, most tiles skip it.
+      if (__builtin_amdgcn_ballot_w64(vis != ~0u) != 0) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int off = 8 * (r >> 2) + (r & 3);
-            pr[r] = keep_if_bit(pr[r], vis, off, 0.f);
-            ds[r] = keep_if_bit(ds[r], vis, off, 0.f);
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int off = 8 * (r >> 2) + (r & 3);
+          pr[r] = keep_if_bit(pr[r], vis, off, 0.f);
+          ds[r] = keep_if_bit(ds[r], vis, off, 0.f);
         }
-        xchg(it, 0) = pack8<v8, T>(pr);
-        xchg(it, 1) = pack8<v8, T>(pr + 8);
-        xchg(it, 2) = pack8<v8, T>(ds);
-        xchg(it, 3) = pack8<v8, T>(ds + 8);
+      }
+      xchg(it, 0) = pack8<v8, T>(pr);
+      xchg(it, 1) = pack8<v8, T>(pr + 8);
+      xchg(it, 2) = pack8<v8, T>(ds);
+      xchg(it, 3) = pack8<v8, T>(ds + 8);
+    };
+    // Two accumulator sets alternate by parity: tile it's products sit in
+    // set it % 2.
+    f32x16 s0, d0, s1, d1;
+    walk2(pre, [&](int it, auto parity) {
+      if constexpr (parity == 0) {
+        if (it == 0 && n > 0) products(0, s0, d0, [](int) {});
+        if (it < n) scores(it, s0, d0, s1, d1);
+      } else {
+        if (it < n) scores(it, s1, d1, s0, d0);
       }
     });
     return;
