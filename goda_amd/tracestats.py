@@ -2,13 +2,16 @@
 
     python -m goda_amd.tracestats trace <kernel_trace.csv> --kernel REGEX [--last N]
     python -m goda_amd.tracestats pmc <counter_collection.csv> [--kernel REGEX] [--last N]
+    python -m goda_amd.tracestats dispatches <kernel_trace.csv> --kernel REGEX
     python -m goda_amd.tracestats copy [--mib 1100] [--reps 3]
 
 `trace` reads a `rocprofv3 --kernel-trace --output-format csv` file and prints,
 per kernel name matching REGEX, the dispatch count and the mean / median /
 min / max duration in microseconds — over the LAST N dispatches when `--last`
 is given (a bench run launches its W warm-up steps first, so `--last K`
-selects exactly the K timed steps). `pmc` reads a `rocprofv3 --pmc` file and
+selects exactly the K timed steps). `dispatches` lists every dispatch of the
+matching kernels in start order with its duration (the warm-up behaviour of a
+process). `pmc` reads a `rocprofv3 --pmc` file and
 prints each counter's mean per dispatch (summed over the XCD / SE instances
 the CSV lists separately), plus the matrix-core utilisation when
 SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE are both present. `copy` runs a
@@ -60,6 +63,19 @@ def kernel_trace(path: str, kernel: str, last: int | None) -> list[dict]:
     return out
 
 
+def dispatch_list(path: str, kernel: str) -> list[tuple[int, str, float]]:
+    pat = re.compile(kernel)
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r.get("Kernel_Name", "")
+            if pat.search(name):
+                start, end = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+                rows.append((start, name, (end - start) / 1e3))
+    rows.sort()
+    return rows
+
+
 def counters(path: str, kernel: str | None, last: int | None) -> dict[str, float]:
     pat = re.compile(kernel) if kernel else None
     per: dict[tuple[int, str], float] = defaultdict(float)
@@ -103,6 +119,9 @@ def main(argv: list[str] | None = None) -> int:
     t.add_argument("csv")
     t.add_argument("--kernel", default=".")
     t.add_argument("--last", type=int, default=None)
+    d = sub.add_parser("dispatches")
+    d.add_argument("csv")
+    d.add_argument("--kernel", default=".")
     p = sub.add_parser("pmc")
     p.add_argument("csv")
     p.add_argument("--kernel", default=None)
@@ -113,6 +132,12 @@ def main(argv: list[str] | None = None) -> int:
     a = ap.parse_args(argv)
     if a.mode == "copy":
         copy_run(a.mib, a.reps)
+        return 0
+    if a.mode == "dispatches":
+        rows = dispatch_list(a.csv, a.kernel)
+        t0 = rows[0][0] if rows else 0
+        for i, (start, name, dur) in enumerate(rows):
+            print(f"{i:4d}  t+{(start - t0) / 1e6:9.3f} ms  {dur:9.1f} us  {name[:70]}")
         return 0
     if a.mode == "trace":
         for s in kernel_trace(a.csv, a.kernel, a.last):
