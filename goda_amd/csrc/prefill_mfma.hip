@@ -465,10 +465,21 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) oacc[md][nt] = f32x16{};
   float m_run[NT], l_run[NT];
+  // Without ALiBi every accumulator of a lane starts at -m of its query row:
+  // minit holds that block and is the C operand of each S tile's first
+  // product, so no VALU instruction refills the accumulators per tile
+  // (cfg2 kernel -1.2%; head_dim 256 has no 16 registers to spare for it).
+  constexpr bool MINIT = !ALIBI && D <= 128;
+  f32x16 minit[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     m_run[nt] = kNegInf;
     l_run[nt] = 0.f;
+    minit[nt] = f32x16{};
+  }
+  if constexpr (MINIT) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(minit[nt]));
   }
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
   const float alibi_s1 = slope2, alibi_s2 = 2.f * slope2, alibi_s3 = 3.f * slope2, alibi_s8 = 8.f * slope2;
@@ -563,7 +574,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
             if ((r & 3) == 0 && (mt | r) != 0) bg += alibi_s8;
             s[mt][nt][r] = (r & 3) == 0 ? bg : (r & 3) == 1 ? bg + alibi_s1 : (r & 3) == 2 ? bg + alibi_s2 : bg + alibi_s3;
           }
-      } else {
+      } else if constexpr (!MINIT) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -576,7 +587,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       for (int mt = 0; mt < MT; ++mt) {
         const v8 av = kp[ks * 2 * BKV + mt * 32];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) s[mt][nt] = mfma32(av, qf[nt][ks], s[mt][nt]);
+        for (int nt = 0; nt < NT; ++nt)
+          s[mt][nt] = mfma32(av, qf[nt][ks], (ks == 0 && MINIT) ? minit[nt] : s[mt][nt]);
       }
   };
 
@@ -649,6 +661,12 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         const float alpha = (m_run[nt] == kNegInf) ? 0.f : fast_exp2(m_run[nt] - mn);
         const float shift = (mn == kNegInf) ? 0.f : mn - mq[nt];
         m_run[nt] = mn;
+        if constexpr (MINIT) {
+          const float mi = (mn == kNegInf) ? 0.f : -mn;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) minit[nt][r] = mi;
+          asm volatile("" : "+v"(minit[nt]));
+        }
         l_run[nt] *= alpha;
 #pragma unroll
         for (int md = 0; md < MD; ++md) oacc[md][nt] *= alpha;
