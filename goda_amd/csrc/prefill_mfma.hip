@@ -518,7 +518,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     for (int i = 0; i < NSTG; ++i) stg[i] = src[i * 64];
   };
   auto tile_store_part = [&](int j, int part) {
-    v8* dst = reinterpret_cast<v8*>(smem + (j % kStages) * TG::BYTES) + my_chunk0 + part * NSTG * 64;
+    v8* dst = reinterpret_cast<v8*>(smem + ((j - j_lo) & (kStages - 1)) * TG::BYTES) + my_chunk0 + part * NSTG * 64;
 #pragma unroll
     for (int i = 0; i < NSTG; ++i) dst[i * 64] = stg[i];
   };
@@ -545,7 +545,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     const unsigned long long base =
         (unsigned long long)(uintptr_t)(ws + ws_tile(b, j, hk, p.ntiles_k, a.heads_kv) * TG::BYTES);
     const unsigned lds0 =
-        (unsigned)(uintptr_t)(smem + (j % kStages) * TG::BYTES) + (unsigned)(wave_u * LOADS * 64 * 16);
+        (unsigned)(uintptr_t)(smem + ((j - j_lo) & (kStages - 1)) * TG::BYTES) + (unsigned)(wave_u * LOADS * 64 * 16);
     dma_blocks<LOADS>(lds0, lane_off, base);
   };
   auto dma_barrier = [&]() { dma_ring_barrier<LOADS>(); };
@@ -555,12 +555,12 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // S^T(j) in log2 units relative to the row's current reference max: the
   // accumulators start at -m (plus the ALiBi bias slope*(kv - i) of each
   // register), so a score leaves the MFMA as the exponent of its P.
-  auto qk = [&](int j, f32x16 (&s)[MT][NT]) {
+  auto qk = [&](int j, f32x16 (&s)[MT][NT], int js) {
     if constexpr (MASK) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) mw[nt] = mrow[nt][j];
     }
-    const v8* kp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES) + hi * BKV + l32;
+    const v8* kp = reinterpret_cast<const v8*>(smem + ((js - j_lo) & (kStages - 1)) * TG::BYTES) + hi * BKV + l32;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const float m0 = (m_run[nt] == kNegInf) ? 0.f : -m_run[nt];
@@ -700,7 +700,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 
   // ---- O^T += V^T P^T for tile j ----------------------------------------------------
   auto pv_mfma = [&](int j, const v8 (&pf)[NT][KS2]) {
-    const v8* vp = reinterpret_cast<const v8*>(smem + (j % kStages) * TG::BYTES + TG::K_CHUNKS * TG::CHB) +
+    const v8* vp = reinterpret_cast<const v8*>(smem + ((j - j_lo) & (kStages - 1)) * TG::BYTES + TG::K_CHUNKS * TG::CHB) +
                    hi * D + l32;
 #pragma unroll
     for (int ks2 = 0; ks2 < KS2; ++ks2) {
@@ -720,7 +720,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // LDS round trip every two MFMAs.
   auto mphase = [&](int j, const v8 (&pf)[NT][KS2], f32x16 (&s)[MT][NT]) {
     pv_mfma(j, pf);
-    qk(j + 1 < j_hi ? j + 1 : j, s);
+    // (the last step's products read stage j + 1 and are never used)
+    qk(j + 1 < j_hi ? j + 1 : j, s, j + 1);
     // counted in instructions: an fp32 step is 8 MFMAs and its 32-byte
     // operand two 16-byte LDS reads
     constexpr int kMfma = (KS2 * MD * NT + KS * MT * NT) * kMfmaPerStep<T>;
@@ -776,7 +777,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       }
     }
     ring_barrier();
-    qk(j_lo, s_a);
+    qk(j_lo, s_a, j_lo);
   }
 
   {
@@ -788,7 +789,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     // Both groups touch tiles j and j+1 in interval j, so the ring is the
     // same for both.
     if (wave >= 4 && ntile > 0) vpart(j_lo, s_a, pf);
-    for (int j = j_lo; j < j_hi; ++j) {
+    auto step = [&](int j) {
       ring_begin(j);
       if (wave < 4) {
         vpart(j, s_a, pf);
@@ -800,6 +801,13 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         if (j + 1 < j_hi) vpart(j + 1, s_a, pf);
       }
       ring_end(j);
+    };
+    // Unrolled by the ring depth, so every stage address is a constant.
+    for (int t = 0; t < ntile; t += kStages) {
+      step(j_lo + t);
+      if (t + 1 < ntile) step(j_lo + t + 1);
+      if (t + 2 < ntile) step(j_lo + t + 2);
+      if (t + 3 < ntile) step(j_lo + t + 3);
     }
   }
 
