@@ -464,7 +464,12 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   for (int md = 0; md < MD; ++md)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) oacc[md][nt] = f32x16{};
-  float m_run[NT], l_run[NT];
+  float m_run[NT];
+  float l_run[NT][4];  // row sum in four independent chains (one per dot-product slot), added at the end
+  // Rescale test of a tile against its own reference: the reference moves
+  // when the tile's max (relative to the reference) exceeds gthr, which is
+  // kRescaleThresh once the row has a finite reference and -inf before.
+  float gthr[NT];
   // Without ALiBi every accumulator of a lane starts at -m of its query row:
   // minit holds that block and is the C operand of each S tile's first
   // product, so no VALU instruction refills the accumulators per tile
@@ -474,7 +479,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     m_run[nt] = kNegInf;
-    l_run[nt] = 0.f;
+    l_run[nt][0] = l_run[nt][1] = l_run[nt][2] = l_run[nt][3] = 0.f;
+    gthr[nt] = kNegInf;
     minit[nt] = f32x16{};
   }
   if constexpr (MINIT) {
@@ -638,8 +644,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         }
       }
     }
-    // row max (absolute, log2 units) and lazy rescale
-    float mtile[NT], mq[NT];
+    // row max (relative to the reference, log2 units) and lazy rescale
+    float mrel[NT];
     bool grow = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -648,26 +654,28 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; r += 2) mx = max3f(mx, s[mt][nt][r], s[mt][nt][r + 1]);
-      mq[nt] = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];  // shift the scores carry
-      mtile[nt] = half_max(mx) + mq[nt];
-      grow = grow || (mtile[nt] > m_run[nt] + kRescaleThresh);
+      mrel[nt] = half_max(mx);
+      grow = grow || (mrel[nt] > gthr[nt]);
     }
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       // the max moved: rescale O and l, and bring the scores to the new
       // reference (rare: the reference only moves by more than the threshold)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const float mn = fmaxf(m_run[nt], mtile[nt]);
+        const float mq = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];  // the reference the scores carry
+        const float mn = fmaxf(m_run[nt], mrel[nt] + mq);
         const float alpha = (m_run[nt] == kNegInf) ? 0.f : fast_exp2(m_run[nt] - mn);
-        const float shift = (mn == kNegInf) ? 0.f : mn - mq[nt];
+        const float shift = (mn == kNegInf) ? 0.f : mn - mq;
         m_run[nt] = mn;
+        gthr[nt] = (mn == kNegInf) ? kNegInf : kRescaleThresh;
         if constexpr (MINIT) {
           const float mi = (mn == kNegInf) ? 0.f : -mn;
 #pragma unroll
           for (int r = 0; r < 16; ++r) minit[nt][r] = mi;
           asm volatile("" : "+v"(minit[nt]));
         }
-        l_run[nt] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) l_run[nt][i] *= alpha;
 #pragma unroll
         for (int md = 0; md < MD; ++md) oacc[md][nt] *= alpha;
 #pragma unroll
@@ -680,8 +688,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       // Four independent row-sum chains (one per dot-product slot) instead of
-      // one chain of 2*MT*4 dependent dot products: cfg2 +1.1-1.5%.
-      float ls[4] = {l_run[nt], 0.f, 0.f, 0.f};
+      // one chain of 2*MT*4 dependent dot products: cfg2 +1.1-1.5%; kept
+      // apart across tiles and added once in the epilogue (cfg2 -0.8%).
+      float (&ls)[4] = l_run[nt];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -694,7 +703,6 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
           pf[nt][2 * mt + h] = pv;
         }
       }
-      l_run[nt] = (ls[0] + ls[1]) + (ls[2] + ls[3]);
     }
   };
 
@@ -816,7 +824,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
              (int64_t)hq * a.o_stride_h;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const float ltot = half_sum(l_run[nt]);
+    const float ltot = half_sum((l_run[nt][0] + l_run[nt][1]) + (l_run[nt][2] + l_run[nt][3]));
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
     const int qi = wrow0 + 32 * nt + l32;
     if (qi < g.lq) {
