@@ -373,7 +373,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   const int l32 = lane & 31;
   const int hi = lane >> 5;  // lane half
   const int hq = hk * p.group + sl * hg + (wave % hg);
-  const int wrow0 = qr0 + (wave / hg) * 32 * NT;  // first query row of this wave
+  const int wrow0 = qr0 + (__builtin_amdgcn_readfirstlane(wave) / hg) * 32 * NT;  // first query row of this wave (scalar)
   const int diag = g.lk - g.lq;
   const bool use_window = a.window_left >= 0 && (a.causal || g.lq == 1);
 
@@ -644,8 +644,11 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
         }
       }
     }
-    // row max (relative to the reference, log2 units) and lazy rescale
-    float mrel[NT];
+    // Row max (relative to the reference, log2 units) and lazy rescale. The
+    // test runs on each lane's half of the row: a row's max exceeds the
+    // threshold iff one of its halves does, and the ballot spans both, so
+    // the two halves are only combined on the (rare) rescale path.
+    float mhalf[NT];
     bool grow = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -654,8 +657,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; r += 2) mx = max3f(mx, s[mt][nt][r], s[mt][nt][r + 1]);
-      mrel[nt] = half_max(mx);
-      grow = grow || (mrel[nt] > gthr[nt]);
+      mhalf[nt] = mx;
+      grow = grow || (mx > gthr[nt]);
     }
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       // the max moved: rescale O and l, and bring the scores to the new
@@ -663,7 +666,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const float mq = (m_run[nt] == kNegInf) ? 0.f : m_run[nt];  // the reference the scores carry
-        const float mn = fmaxf(m_run[nt], mrel[nt] + mq);
+        const float mn = fmaxf(m_run[nt], half_max(mhalf[nt]) + mq);
         const float alpha = (m_run[nt] == kNegInf) ? 0.f : fast_exp2(m_run[nt] - mn);
         const float shift = (mn == kNegInf) ? 0.f : mn - mq;
         m_run[nt] = mn;
