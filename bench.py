@@ -373,11 +373,12 @@ def main() -> int:
     steps, warmup = args.steps, args.warmup
     out: dict = {}
     # The two roofline lines (cfg4 decode, then the cfg2 prefill headline)
-    # are measured last of the GPU work: the first ~40 ms of GPU load in a
-    # process run the kernels slower while the GPU leaves its idle clock state
-    # (per-dispatch trace of a cold process: the cfg2 attention kernel at
-    # 2098 us on the first dispatch, ~1840 us from about the 20th on), and the
-    # other configs' own warm-up and timed steps cover that.
+    # are measured last of the GPU work. In a fresh process the attention
+    # kernels run slower for their first ~20 dispatches (cfg2 kernel, cold
+    # process: 2117, 2569, 2322, 2245, 2136, 2018 us ... ~1880 us from about
+    # the 20th dispatch on; neither a pause after the inputs are made, a pass
+    # over them, nor 0.1 s of other matrix products first changes that), and
+    # the other configs' own steps run through most of it.
     if args.only in (None, "cfg3"):
         _log("bench: cfg3 prefill")
         out["cfg3"] = bench_prefill(wl.CFG3, steps, warmup)
