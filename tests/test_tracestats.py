@@ -1,0 +1,75 @@
+"""CPU tests of goda_amd.tracestats, the summariser behind profiles/ (rocprofv3
+CSV files are synthesised here with the columns the tool reads)."""
+
+from __future__ import annotations
+
+import csv
+
+import pytest
+
+from goda_amd import tracestats as ts
+
+
+def _write(path, header, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(header)
+        w.writerows(rows)
+
+
+@pytest.fixture()
+def trace_csv(tmp_path):
+    p = tmp_path / "kt_kernel_trace.csv"
+    rows = []
+    # kernel A: 5 dispatches of 10, 20, 30, 40, 50 us, listed out of order
+    for i, d in [(2, 30), (0, 10), (4, 50), (1, 20), (3, 40)]:
+        start = 1_000_000 * i
+        rows.append(["kern_A<bf16>", start, start + d * 1000])
+    # kernel B: 2 dispatches of 7 us
+    for i in range(2):
+        start = 500_000 + 1_000_000 * i
+        rows.append(["kern_B", start, start + 7000])
+    _write(p, ["Kernel_Name", "Start_Timestamp", "End_Timestamp"], rows)
+    return str(p)
+
+
+def test_trace_summarises_the_last_dispatches_in_start_order(trace_csv):
+    out = {s["kernel"]: s for s in ts.kernel_trace(trace_csv, "kern_", last=3)}
+    a = out["kern_A<bf16>"]
+    assert a["dispatches"] == 5 and a["summarised"] == 3
+    assert a["mean_us"] == pytest.approx(40.0)  # the last three by start time: 30, 40, 50
+    assert (a["min_us"], a["max_us"], a["median_us"]) == (30.0, 50.0, 40.0)
+    b = out["kern_B"]
+    assert b["dispatches"] == 2 and b["summarised"] == 2 and b["mean_us"] == pytest.approx(7.0)
+
+
+def test_trace_filters_by_regex(trace_csv):
+    names = [s["kernel"] for s in ts.kernel_trace(trace_csv, "kern_B", last=None)]
+    assert names == ["kern_B"]
+
+
+def test_dispatches_lists_every_dispatch_in_start_order(trace_csv):
+    rows = ts.dispatch_list(trace_csv, "kern_A")
+    assert [d for _, _, d in rows] == [10.0, 20.0, 30.0, 40.0, 50.0]
+    starts = [s for s, _, _ in rows]
+    assert starts == sorted(starts)
+
+
+def test_pmc_sums_instances_per_dispatch_and_derives_mfma_busy(tmp_path):
+    p = tmp_path / "p_counter_collection.csv"
+    rows = []
+    # two dispatches; each counter split over two instances (e.g. two XCDs)
+    for disp, scale in [(1, 1.0), (2, 3.0)]:
+        for inst in range(2):
+            rows.append([disp, "prefill_fa_kernel", "GRBM_GUI_ACTIVE", 4000.0 * scale])
+            rows.append([disp, "prefill_fa_kernel", "SQ_VALU_MFMA_BUSY_CYCLES", 256000.0 * scale])
+        rows.append([disp, "other_kernel", "GRBM_GUI_ACTIVE", 1.0])
+    _write(p, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"], rows)
+    avg = ts.counters(str(p), "prefill_fa", last=None)
+    assert avg["dispatches"] == 2
+    assert avg["GRBM_GUI_ACTIVE"] == pytest.approx(8000.0 * 2.0)  # mean over dispatches of the instance sums
+    assert avg["SQ_VALU_MFMA_BUSY_CYCLES"] == pytest.approx(512000.0 * 2.0)
+    # busy / (GRBM cycles per XCD x 1024 SIMDs)
+    assert avg["mfma_busy_frac"] == pytest.approx(1024000.0 / (16000.0 / ts.XCDS * ts.SIMDS))
+    last = ts.counters(str(p), "prefill_fa", last=1)
+    assert last["dispatches"] == 1 and last["GRBM_GUI_ACTIVE"] == pytest.approx(24000.0)
