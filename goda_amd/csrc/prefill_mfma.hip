@@ -379,7 +379,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
 
   // ---- Q^T operand fragments (rotated) ---------------------------------------
   v8 qf[NT][KS];
-  {
+  // (invoked in the prologue, after the first tiles' copies are issued)
+  auto load_q = [&]() {
     const T* qbase = reinterpret_cast<const T*>(a.q) +
                      (a.cu_seqlens_q ? 0 : (int64_t)b * a.q_stride_b) + (int64_t)hq * a.q_stride_h;
 #pragma unroll
@@ -448,7 +449,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qf[nt][ks]));
-  }
+  };
 
   // ---- key tile range ---------------------------------------------------------
   const int q_last = min(qr0 + qb_rows, g.lq) - 1;
@@ -780,8 +781,10 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   if (ntile > 0) {
     if constexpr (DMA) {
       for (int t = 0; t < kAhead && t < ntile; ++t) tile_dma(j_lo + t);
+      load_q();
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
+      load_q();
       for (int t = 0; t < kAhead && t < ntile; ++t) {
         tile_load(j_lo + t);
         tile_store(j_lo + t);
