@@ -1210,28 +1210,32 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
   const int i = wrow0 + l32;
   const int iabs = diag + i;
 
-  // B operands of this wave's 32 rows: q (rotated) and dO, plus statistics.
+  // B operands of this wave's 32 rows: q (rotated) and dO, plus statistics
+  // (loaded after the first key tile's copy is issued, so the latencies
+  // overlap).
   v8 qf[KS], gf[KS];
   float l2 = kNegInf, dl = 0.f;
-  if (wrow0 < g.lq) {
-    const v8* img = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, wrow0 / kQRows, hq, p.ntq, a.heads_q) * QI::BYTES);
+  auto load_qg = [&]() {
+    if (wrow0 < g.lq) {
+      const v8* img = reinterpret_cast<const v8*>(p.qimg + q_tile_index(b, wrow0 / kQRows, hq, p.ntq, a.heads_q) * QI::BYTES);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = img[QI::QA + (2 * ks + hi) * kQRows + (l32 ^ (QI::SWZ * hi))];
+        gf[ks] = img[QI::GA + (2 * ks + hi) * kQRows + (l32 ^ (QI::SWZ * hi))];
+      }
+      const float* stat = reinterpret_cast<const float*>(img + QI::STAT);
+      l2 = stat[l32];
+      dl = stat[kQRows + l32];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = gf[ks] = v8{};
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = img[QI::QA + (2 * ks + hi) * kQRows + (l32 ^ (QI::SWZ * hi))];
-      gf[ks] = img[QI::GA + (2 * ks + hi) * kQRows + (l32 ^ (QI::SWZ * hi))];
+      asm volatile("" : "+v"(qf[ks]));
+      asm volatile("" : "+v"(gf[ks]));
     }
-    const float* stat = reinterpret_cast<const float*>(img + QI::STAT);
-    l2 = stat[l32];
-    dl = stat[kQRows + l32];
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = gf[ks] = v8{};
-  }
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    asm volatile("" : "+v"(qf[ks]));
-    asm volatile("" : "+v"(gf[ks]));
-  }
+  };
   const float slope2 = ALIBI ? a.alibi_slopes[hq] * kLog2e : 0.f;
   // The caller's mask row of this lane's query row (rows past the sequence
   // read the last row's bits and are masked anyway): one word per key tile.
@@ -1364,12 +1368,14 @@ __global__ void __launch_bounds__((DqShape<T, D>::WAVES * 64), (DqShape<T, D>::O
     // barrier opening the interval ends every read of tile it - 1 there, and
     // the one opening interval it + 1 waits for the copies (vmcnt(0)).
     if (n > 0) tile_dma(0);
+    load_qg();
     for (int it = 0; it < n; ++it) {
       dma_ring_barrier<0>();
       if (it + 1 < n) tile_dma(it + 1);
       compute(it);
     }
   } else {
+    load_qg();
     if (n > 0) {
       tile_load(0);
       tile_store(0);
