@@ -738,7 +738,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
     // operand two 16-byte LDS reads
     constexpr int kMfma = (KS2 * MD * NT + KS * MT * NT) * kMfmaPerStep<T>;
     constexpr int kReads = (KS2 * MD + KS * MT) * TG::CHB / 16;
-    constexpr int kLead = 4;
+    // (same-box A/B: at D = 128, 4 beats 2, 6 and 8 by 0.5-0.7%; at D = 256,
+    // 3 beats 4 by 6.4% on cfg3 and ties on cfg5)
+    constexpr int kLead = D >= 256 ? 3 : 4;
     static_assert(kReads > kLead, "phase too short");
     __builtin_amdgcn_sched_group_barrier(0x100, kLead, 0);
 #pragma unroll
