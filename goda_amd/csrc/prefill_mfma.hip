@@ -540,9 +540,11 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // 16-bit tiles move by direct global->LDS loads instead (dma_blocks): wave
   // w's share of a tile is LOADS blocks of 64 consecutive 16-byte chunks, the
   // same offsets in the workspace tile and in the LDS stage. The ring barrier
-  // waits vmcnt(LOADS): every batch but the newest one has landed. A tile
-  // lands in stage (j + kAhead) % kStages, which no wave reads between its
-  // issue (interval j, after the barrier) and the barrier opening interval
+  // waits vmcnt(LOADS): every batch but the newest one has landed. Tile t
+  // sits in stage (t - j_lo) mod kStages (counted from the workgroup's first
+  // tile, so the loop unrolled by kStages sees constant stage addresses);
+  // tile j + kAhead lands in a stage no wave reads between its issue
+  // (interval j, after the barrier) and the barrier opening interval
   // j + kAhead - 1, where it is first read.
   constexpr bool DMA = sizeof(T) == 2;
   static_assert(!DMA || LOADS == 2 || LOADS == 4, "DMA share of 2 or 4 blocks");
@@ -562,6 +564,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) prefill_fa_kernel(const Prefill
   // S^T(j) in log2 units relative to the row's current reference max: the
   // accumulators start at -m (plus the ALiBi bias slope*(kv - i) of each
   // register), so a score leaves the MFMA as the exponent of its P.
+  // js is the tile whose stage the products read: j itself, except on a
+  // wave's last step, where j is clamped for the mask words and the bias and
+  // the products read stage j + 1 (whatever it holds; they are never used).
   auto qk = [&](int j, f32x16 (&s)[MT][NT], int js) {
     if constexpr (MASK) {
 #pragma unroll
