@@ -127,6 +127,28 @@ def test_backward_workgroup_order_partial_chunks():
     _case(3, 70, 70, 12, 6, 128, torch.float32, causal=True, seed=23)
 
 
+@pytest.mark.parametrize("d,hq,hkv,alibi", [(128, 8, 2, False), (256, 16, 1, True)])
+def test_forward_backward_run_to_run_bit_identical(d, hq, hkv, alibi):
+    """No atomics or order-dependent sums anywhere on the path: two calls on
+    the same inputs give the same bits (o, lse, dq, dk, dv), including the
+    head_dim-256 dk/dv walk split over workgroups whose fp32 partials a
+    separate pass sums in a fixed order."""
+    b, t, dtype = 2, 1000, torch.bfloat16
+    q = _rand((b, t, hq, d), dtype, 31).to(DEV)
+    k = _rand((b, t, hkv, d), dtype, 32).to(DEV)
+    v = _rand((b, t, hkv, d), dtype, 33).to(DEV)
+    d_o = _rand((b, t, hq, d), dtype, 34, std=1.0).to(DEV)
+    kw = {"alibi_slopes": torch.tensor(wl.alibi_slopes(hq), dtype=torch.float32, device=DEV)} if alibi else {}
+    runs = []
+    for _ in range(2):
+        o, lse = ops.attention_prefill(q, k, v, causal=True, return_lse=True, **kw)
+        runs.append((o, lse) + tuple(ops.attention_prefill_bwd(q, k, v, o, lse, d_o, causal=True, **kw)))
+    torch.cuda.synchronize()
+    for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), runs[0], runs[1]):
+        assert torch.isfinite(x).all() and x.abs().max().item() > 0, name
+        assert torch.equal(x, y), f"{name} differs between two calls (d={d})"
+
+
 def test_backward_rows_without_keys():
     """Lq > Lk with causal: the first Lq - Lk rows see no key; their o is 0
     and they contribute nothing (checked against the float64 brute force)."""
